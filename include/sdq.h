@@ -1,0 +1,266 @@
+/*
+ * sdq.h -- C ABI of libsdq, the MI355X (gfx950) backend for the MLX-affine
+ * quantized linear of stable-diffusion.rs.
+ *
+ * The reference binds mlx-c by hand (crates/sd-tensor/src/mlx.rs:21-22,
+ * 106-417) and reaches the quantized path through five groups of calls:
+ * handles and dtypes, array lifecycle, streams/eval, the error handler, and
+ * the three quantization ops.  Every entry point below replaces one of those
+ * bindings one for one -- same argument order, same meaning, same
+ * status/ownership rules -- so the Rust crate binds this header exactly as it
+ * binds mlx-c today, with the prefix changed.  Each declaration cites the
+ * binding it replaces.
+ *
+ * Conventions (mirroring mlx-c, as the reference relies on them):
+ *   - handles are `struct { void* ctx; }` passed by value (mlx.rs:38-98);
+ *   - ops return int status, 0 = success; on failure the message goes,
+ *     synchronously and on the calling thread, to the handler installed with
+ *     sdq_set_error_handler (mlx.rs:412-470), and the result is left as it was;
+ *   - results come back through out-pointers; a result handle whose ctx is
+ *     NULL gets a new array, an existing one is overwritten (mlx.rs:1923);
+ *   - every handle returned is owned by the caller and released exactly once
+ *     with its *_free (mlx.rs:1448-1452);
+ *   - arrays live in device memory (HBM).  Ops are enqueued on the stream
+ *     and run asynchronously; sdq_eval / sdq_synchronize / the data accessors
+ *     are true device synchronisations, so MLX's lazy-then-eval semantics
+ *     (mlx.rs:8-13, 1531-1544) hold for a caller;
+ *   - there is no CPU backend.  A CPU stream is accepted as a handle (the
+ *     reference creates one, mlx.rs:491-494) but every op submitted to it
+ *     fails with a message; nothing silently falls back to host code.
+ */
+#ifndef SDQ_H
+#define SDQ_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- handles: mlx.rs:38-98 ----------------------------------------------- */
+
+/* replaces mlx_array (mlx.rs:38-42) */
+typedef struct sdq_array_ {
+  void *ctx;
+} sdq_array;
+
+/* replaces mlx_stream (mlx.rs:44-48) */
+typedef struct sdq_stream_ {
+  void *ctx;
+} sdq_stream;
+
+/* replaces mlx_vector_array (mlx.rs:50-54) */
+typedef struct sdq_vector_array_ {
+  void *ctx;
+} sdq_vector_array;
+
+/* replaces mlx_optional_int (mlx.rs:56-72): an int then a bool, by value */
+typedef struct sdq_optional_int_ {
+  int value;
+  bool has_value;
+} sdq_optional_int;
+
+/* replaces mlx_optional_dtype (mlx.rs:74-80) */
+typedef struct sdq_optional_dtype_ {
+  int value;
+  bool has_value;
+} sdq_optional_dtype;
+
+/* Positions are those of mlx_dtype (mlx.rs:100-104: INT32=7, FLOAT16=9,
+ * FLOAT32=10), so the Rust constants carry over unchanged. */
+typedef enum sdq_dtype_ {
+  SDQ_BOOL = 0,
+  SDQ_UINT8 = 1,
+  SDQ_UINT16 = 2,
+  SDQ_UINT32 = 3,
+  SDQ_UINT64 = 4,
+  SDQ_INT8 = 5,
+  SDQ_INT16 = 6,
+  SDQ_INT32 = 7,
+  SDQ_INT64 = 8,
+  SDQ_FLOAT16 = 9,
+  SDQ_FLOAT32 = 10,
+  SDQ_FLOAT64 = 11,
+  SDQ_BFLOAT16 = 12,
+  SDQ_COMPLEX64 = 13
+} sdq_dtype;
+
+/* ---- errors: mlx.rs:412-416 ------------------------------------------------ */
+
+typedef void (*sdq_error_handler_func)(const char *msg, void *data);
+
+/* replaces mlx_set_error_handler (mlx.rs:412-416).  Process-wide; NULL
+ * restores the default handler (print to stderr).  The previous handler's
+ * dtor, if any, is called on its data. */
+void sdq_set_error_handler(sdq_error_handler_func handler, void *data,
+                           void (*dtor)(void *));
+
+/* ---- arrays: mlx.rs:106-121, 558-612 --------------------------------------- */
+
+/* An empty handle (mlx-c's mlx_array_new). */
+sdq_array sdq_array_new(void);
+/* replaces mlx_array_new_data (mlx.rs:109-114): copies `data` (host memory,
+ * row-major, shape[0..dim)) into a new device array.  On error the returned
+ * ctx is NULL and the handler has the message (mlx.rs:572-577). */
+sdq_array sdq_array_new_data(const void *data, const int *shape, int dim,
+                             sdq_dtype dtype);
+/* replaces mlx_array_new_float32 (mlx.rs:115): a 0-d f32 array. */
+sdq_array sdq_array_new_float32(float val);
+/* replaces mlx_array_free (mlx.rs:116) */
+int sdq_array_free(sdq_array arr);
+/* replaces mlx_array_size (mlx.rs:117) */
+size_t sdq_array_size(sdq_array arr);
+/* replaces mlx_array_ndim (mlx.rs:118) */
+size_t sdq_array_ndim(sdq_array arr);
+/* replaces mlx_array_shape (mlx.rs:119): valid while the array lives */
+const int *sdq_array_shape(sdq_array arr);
+/* replaces mlx_array_dtype (mlx.rs:120) */
+sdq_dtype sdq_array_dtype(sdq_array arr);
+size_t sdq_array_nbytes(sdq_array arr);
+/* Waits for the work that produces `arr` (mlx-c's mlx_array_eval). */
+int sdq_array_eval(sdq_array arr);
+/* replaces mlx_array_data_float32 (mlx.rs:121): synchronises, copies the
+ * contents to a host mirror owned by the array and returns it (valid until
+ * the array is freed or written again).  NULL, with a message, if the dtype
+ * is not float32. */
+const float *sdq_array_data_float32(sdq_array arr);
+/* The same for uint32 (packed weights) and for the 16-bit float types, whose
+ * elements are returned as raw bit patterns. */
+const uint32_t *sdq_array_data_uint32(sdq_array arr);
+const uint16_t *sdq_array_data_bfloat16(sdq_array arr);
+const uint16_t *sdq_array_data_float16(sdq_array arr);
+/* Copies the contents to caller memory; nbytes must equal sdq_array_nbytes. */
+int sdq_array_copy_to_host(void *dst, size_t nbytes, sdq_array arr);
+
+/* ---- vectors of arrays: mlx.rs:341-342, 358-359, 398 ----------------------- */
+
+sdq_vector_array sdq_vector_array_new(void);                     /* mlx.rs:342 */
+sdq_vector_array sdq_vector_array_new_value(sdq_array val);      /* mlx.rs:341 */
+int sdq_vector_array_append_value(sdq_vector_array vec, sdq_array val);
+size_t sdq_vector_array_size(sdq_vector_array vec);              /* mlx.rs:358 */
+int sdq_vector_array_get(sdq_array *res, sdq_vector_array vec,   /* mlx.rs:359 */
+                         size_t index);
+int sdq_vector_array_free(sdq_vector_array vec);                 /* mlx.rs:398 */
+
+/* ---- streams and evaluation: mlx.rs:338-340, 399 ---------------------------- */
+
+/* replaces mlx_default_gpu_stream_new (mlx.rs:338): a handle on the current
+ * device's default HIP stream (one per device, created on first use, default
+ * priority). */
+sdq_stream sdq_default_gpu_stream_new(void);
+/* replaces mlx_default_cpu_stream_new (mlx.rs:339).  See the note on the CPU
+ * backend at the top of this file. */
+sdq_stream sdq_default_cpu_stream_new(void);
+/* A handle on a new HIP stream of its own on the current device. */
+sdq_stream sdq_gpu_stream_new(void);
+/* replaces mlx_stream_free (mlx.rs:340) */
+int sdq_stream_free(sdq_stream s);
+/* Blocks until everything enqueued on `s` has finished. */
+int sdq_synchronize(sdq_stream s);
+/* The hipStream_t behind a GPU stream (NULL for the CPU stream), for callers
+ * that time or order work with HIP events of their own. */
+void *sdq_stream_native(sdq_stream s);
+/* replaces mlx_eval (mlx.rs:399): waits for the work producing each array. */
+int sdq_eval(sdq_vector_array outputs);
+
+/* ---- memory accounting: mlx.rs:405-411 ---------------------------------------- */
+
+int sdq_get_active_memory(size_t *res);          /* mlx.rs:405 */
+int sdq_get_peak_memory(size_t *res);            /* mlx.rs:406 */
+int sdq_get_cache_memory(size_t *res);           /* mlx.rs:407 */
+int sdq_reset_peak_memory(void);                 /* mlx.rs:408 */
+int sdq_set_cache_limit(size_t *res, size_t limit); /* mlx.rs:410 */
+int sdq_clear_cache(void);                       /* mlx.rs:411 */
+
+/* ---- the quantized path: mlx.rs:361-397 -------------------------------------- */
+
+/* replaces mlx_quantize (mlx.rs:363-371; called at mlx.rs:1871-1879).
+ * w: [..., K] float32/bfloat16/float16, K % group_size == 0.
+ * res: a vector of three arrays -- packed weight [..., K*bits/32] uint32,
+ * scales and biases [..., K/group_size] in w's dtype.  group_size defaults to
+ * 64 and may be 32, 64 or 128; bits defaults to 4 and may be 2, 4 or 8;
+ * mode must be "affine" (or NULL); global_scale must be empty (ctx NULL). */
+int sdq_quantize(sdq_vector_array *res, sdq_array w,
+                 sdq_optional_int group_size, sdq_optional_int bits,
+                 const char *mode, sdq_array global_scale, sdq_stream s);
+
+/* replaces mlx_dequantize (mlx.rs:373-384; called at mlx.rs:1926-1940).
+ * res: [..., K] in the scales' dtype, or in `dtype` when it has a value. */
+int sdq_dequantize(sdq_array *res, sdq_array w, sdq_array scales,
+                   sdq_array biases, sdq_optional_int group_size,
+                   sdq_optional_int bits, const char *mode,
+                   sdq_array global_scale, sdq_optional_dtype dtype,
+                   sdq_stream s);
+
+/* replaces mlx_quantized_matmul (mlx.rs:386-397; called at mlx.rs:1959-1970).
+ * y = x @ dequantize(w).T for transpose == true (the only form the reference
+ * uses, mlx.rs:1947-1951).  x: [..., K]; w [N, K*bits/32]; y: [..., N] in the
+ * promotion of x's and the scales' dtypes.  transpose == false is rejected
+ * with a message. */
+int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w,
+                         sdq_array scales, sdq_array biases, bool transpose,
+                         sdq_optional_int group_size, sdq_optional_int bits,
+                         const char *mode, sdq_stream s);
+
+/* ---- elementwise ops the linear and its callers use ------------------------- */
+
+/* replaces mlx_add (mlx.rs:124) for the shapes the quantized linear needs:
+ * equal shapes, or b broadcast along the last axis of a (the bias add after
+ * the matmul, quantized.rs:314-317). */
+int sdq_add(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s);
+/* replaces mlx_multiply (mlx.rs:126), equal shapes (T5's gate, t5.rs:211) */
+int sdq_multiply(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s);
+/* replaces mlx_astype (mlx.rs:149) between float32, bfloat16 and float16 */
+int sdq_astype(sdq_array *res, sdq_array a, sdq_dtype dtype, sdq_stream s);
+/* replaces mlx_contiguous (mlx.rs:150-155).  Arrays made here are always
+ * row-major, so this is a copy. */
+int sdq_contiguous(sdq_array *res, sdq_array a, bool allow_col_major,
+                   sdq_stream s);
+/* Array::gelu_approx (mlx.rs:1041-1054) as one fused op: the reference
+ * composes it from mlx_multiply/add/tanh; the value is the same formula. */
+int sdq_gelu_approx(sdq_array *res, sdq_array a, sdq_stream s);
+/* a @ b.T with f32 accumulation: the dense linear `x @ w.T`
+ * (sd-models/src/mlx/mod.rs:181-189), which the reference composes from
+ * mlx_transpose_axes (mlx.rs:142) and mlx_matmul (mlx.rs:241).  a: [..., K],
+ * b: [N, K]; result [..., N]. */
+int sdq_matmul_nt(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s);
+
+/* ---- raw-pointer entry point ------------------------------------------------- */
+
+/* The kernel behind sdq_quantized_matmul on caller-owned device memory:
+ * y[M, N] (y_dtype) = x[M, K] (x_dtype, row stride ldx elements) @
+ * dequantize(w[N, K*bits/32], scales/biases[N, K/group_size] (s_dtype)).T,
+ * enqueued on `hip_stream` (a hipStream_t; NULL = the default stream).  The
+ * dtypes must be float32, bfloat16 or float16; y_dtype is free.  Scratch
+ * memory, when a shape needs it, comes from the library's cache. */
+int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype,
+                             int64_t ldx, const uint32_t *w,
+                             const void *scales, const void *biases,
+                             int s_dtype, int64_t M, int64_t N, int64_t K,
+                             int group_size, int bits, void *hip_stream);
+
+/* tanh-GELU on caller-owned device memory (dtype float32/bfloat16/float16),
+ * enqueued on `hip_stream`: the elementwise step between the two Flux MLP
+ * linears (flux.rs:400-413) without an array handle. */
+int sdq_gelu_approx_raw(void *out, const void *in, int dtype, int64_t n,
+                        void *hip_stream);
+
+/* The device address of an array's data (valid while the array lives), for
+ * callers that pass it to the raw entry points or to other HIP code.  Has no
+ * mlx-c counterpart: MLX arrays live in unified memory. */
+void *sdq_array_device_ptr(sdq_array arr);
+
+/* ---- library information ----------------------------------------------------- */
+
+/* "sdq <version> gfx950" */
+const char *sdq_version(void);
+/* Number of HIP devices visible (0 when none); never fails. */
+int sdq_device_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDQ_H */

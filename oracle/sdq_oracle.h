@@ -1,0 +1,101 @@
+/*
+ * sdq_oracle.h -- CPU restatement of the MLX-affine quantized linear.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP path is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library (libsdq.so) never links,
+ * loads or calls it, and has no CPU fallback of any kind.
+ *
+ * What it restates (reference paths relative to andreinknv/stable-diffusion.rs):
+ *   - SeededRng: splitmix64 + Box-Muller, cos then sin, f64 math cast to f32
+ *       crates/sd-tensor/src/lib.rs:105-145
+ *   - QuantizedArray::quantize / dequantize / matmul, mode "affine"
+ *       crates/sd-tensor/src/mlx.rs:1856-1975 (the arithmetic itself lives in
+ *       MLX's CPU backend, which is not vendored; restated below)
+ *   - QuantizedArray::resident_bytes   crates/sd-tensor/src/mlx.rs:1977-1985
+ *   - Array::gelu_approx               crates/sd-tensor/src/mlx.rs:1041-1054
+ *
+ * Pinning status of each function is recorded beside it and in the tests
+ * (tests/test_oracle.py).  Every function here is checked there against
+ * known-answer vectors, closed forms or brute force; none is "unpinned" with
+ * respect to the written specification.  Byte equality with real MLX cannot
+ * be checked anywhere (MLX is absent), so the specification choices are
+ * listed at the top of sdq_oracle.c.
+ *
+ * dtype codes are the positions of mlx_dtype (crates/sd-tensor/src/mlx.rs:100-104):
+ *   3 = uint32, 9 = float16, 10 = float32, 12 = bfloat16.
+ */
+#ifndef SDQ_ORACLE_H
+#define SDQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { SDO_UINT32 = 3, SDO_FLOAT16 = 9, SDO_FLOAT32 = 10, SDO_BFLOAT16 = 12 };
+
+/* ---- SeededRng (lib.rs:105-145) ---------------------------------------- */
+uint64_t sdo_rng_next_u64(uint64_t *state);
+double sdo_rng_next_f64(uint64_t *state);
+/* Fills out[0..n) exactly as SeededRng::normals(n) does and advances state. */
+void sdo_rng_normals(uint64_t *state, float *out, size_t n);
+
+/* ---- 16-bit float storage helpers (round to nearest even) -------------- */
+uint16_t sdo_bf16_from_f32(float f);
+float sdo_f32_from_bf16(uint16_t h);
+uint16_t sdo_f16_from_f32(float f);
+float sdo_f32_from_f16(uint16_t h);
+/* Round an f32 value to the given storage dtype and widen it back. */
+float sdo_round_to(float v, int dtype);
+
+/* ---- the path -------------------------------------------------------- */
+/* w [rows, cols] given as f32 values (already exact widenings when the
+ * source is bf16/f16).  Writes wq [rows, cols*bits/32] uint32 and
+ * scales/biases [rows, cols/group_size] in store_dtype (f32: float*,
+ * bf16/f16: uint16_t*).  Returns 0, or -1 on an invalid argument. */
+int sdo_quantize(const float *w, int64_t rows, int64_t cols, int group_size,
+                 int bits, int store_dtype, uint32_t *wq, void *scales,
+                 void *biases);
+
+/* out[r, c] = round_T(round_T(q * s) + b) with T = scale_dtype, returned
+ * widened to f32.  Returns 0, or -1 on an invalid argument. */
+int sdo_dequantize(const uint32_t *wq, const void *scales, const void *biases,
+                   int scale_dtype, int64_t rows, int64_t cols, int group_size,
+                   int bits, float *out);
+
+/* y[m, n] = sum_k x[m, k] * w[n, k], w the f32 dequantized weight,
+ * accumulated in f32 in increasing k (the order of MLX's CPU qmm_t).
+ * x, scales, biases are f32 (MLX promotes x and the scales to one type). */
+int sdo_qmatmul(const float *x, int64_t M, int64_t K, const uint32_t *wq,
+                const float *scales, const float *biases, int64_t N,
+                int group_size, int bits, float *y);
+
+/* The same sums in f64 (an accuracy reference, not MLX's order). */
+int sdo_qmatmul_f64(const float *x, int64_t M, int64_t K, const uint32_t *wq,
+                    const float *scales, const float *biases, int64_t N,
+                    int group_size, int bits, double *y);
+
+/* sdo_qmatmul blocked over N and parallel over `threads` OpenMP threads.
+ * Each output is the same f32 sum in the same k order, so the result is
+ * bit-identical to sdo_qmatmul.  This is the timed CPU baseline. */
+int sdo_qmatmul_omp(const float *x, int64_t M, int64_t K, const uint32_t *wq,
+                    const float *scales, const float *biases, int64_t N,
+                    int group_size, int bits, float *y, int threads);
+
+/* Bytes a quantized weight holds (mlx.rs:1977-1985): packed words * 4 plus
+ * (scales + biases) * 4. */
+uint64_t sdo_resident_bytes(int64_t rows, int64_t cols, int group_size,
+                            int bits);
+
+/* 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))) evaluated op by op in f32 in the
+ * order of mlx.rs:1048-1053. */
+void sdo_gelu_approx(const float *x, float *y, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

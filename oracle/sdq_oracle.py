@@ -1,0 +1,187 @@
+"""numpy-facing wrapper of the CPU oracle (oracle/_build/libsdq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product library never loads
+it.  See sdq_oracle.h for what each function restates and where from.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "libsdq_oracle.so"
+
+UINT32, FLOAT16, FLOAT32, BFLOAT16 = 3, 9, 10, 12
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile the oracle with its Makefile (gcc; no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, c_int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.sdo_rng_next_u64.restype = ctypes.c_uint64
+        L.sdo_rng_next_u64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.sdo_rng_next_f64.restype = ctypes.c_double
+        L.sdo_rng_next_f64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.sdo_rng_normals.restype = None
+        L.sdo_rng_normals.argtypes = [ctypes.POINTER(ctypes.c_uint64), vp, ctypes.c_size_t]
+        L.sdo_quantize.restype = c_int
+        L.sdo_quantize.argtypes = [vp, i64, i64, c_int, c_int, c_int, vp, vp, vp]
+        L.sdo_dequantize.restype = c_int
+        L.sdo_dequantize.argtypes = [vp, vp, vp, c_int, i64, i64, c_int, c_int, vp]
+        L.sdo_qmatmul.restype = c_int
+        L.sdo_qmatmul.argtypes = [vp, i64, i64, vp, vp, vp, i64, c_int, c_int, vp]
+        L.sdo_qmatmul_f64.restype = c_int
+        L.sdo_qmatmul_f64.argtypes = [vp, i64, i64, vp, vp, vp, i64, c_int, c_int, vp]
+        L.sdo_qmatmul_omp.restype = c_int
+        L.sdo_qmatmul_omp.argtypes = [vp, i64, i64, vp, vp, vp, i64, c_int, c_int, vp, c_int]
+        L.sdo_resident_bytes.restype = ctypes.c_uint64
+        L.sdo_resident_bytes.argtypes = [i64, i64, c_int, c_int]
+        L.sdo_gelu_approx.restype = None
+        L.sdo_gelu_approx.argtypes = [vp, vp, ctypes.c_size_t]
+        for n in ("sdo_bf16_from_f32", "sdo_f16_from_f32"):
+            getattr(L, n).restype = ctypes.c_uint16
+            getattr(L, n).argtypes = [ctypes.c_float]
+        for n in ("sdo_f32_from_bf16", "sdo_f32_from_f16"):
+            getattr(L, n).restype = ctypes.c_float
+            getattr(L, n).argtypes = [ctypes.c_uint16]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> ctypes.c_void_p:
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Rng:
+    """SeededRng (crates/sd-tensor/src/lib.rs:105-145)."""
+
+    def __init__(self, seed: int):
+        self.state = ctypes.c_uint64(seed)
+
+    def next_u64(self) -> int:
+        return lib().sdo_rng_next_u64(ctypes.byref(self.state))
+
+    def next_f64(self) -> float:
+        return lib().sdo_rng_next_f64(ctypes.byref(self.state))
+
+    def normals(self, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().sdo_rng_normals(ctypes.byref(self.state), _p(out), n)
+        return out
+
+
+def normals(seed: int, n: int, scale: float = 1.0) -> np.ndarray:
+    v = Rng(seed).normals(n)
+    if scale != 1.0:
+        v = (v * np.float32(scale)).astype(np.float32)
+    return v
+
+
+def _store_np(dtype: int):
+    return np.float32 if dtype == FLOAT32 else np.uint16
+
+
+def quantize(w: np.ndarray, group_size: int = 64, bits: int = 4, store_dtype: int = FLOAT32):
+    """w [rows, cols] (f32 values) -> (wq uint32, scales, biases); scales and
+    biases as f32 arrays, or raw uint16 bits for bf16/f16 storage."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    wq = np.zeros((rows, cols * bits // 32), dtype=np.uint32)
+    sc = np.zeros((rows, cols // group_size), dtype=_store_np(store_dtype))
+    bi = np.zeros_like(sc)
+    rc = lib().sdo_quantize(_p(w), rows, cols, group_size, bits, store_dtype, _p(wq), _p(sc), _p(bi))
+    if rc != 0:
+        raise ValueError("oracle quantize rejected its arguments")
+    return wq, sc, bi
+
+
+def dequantize(wq, scales, biases, group_size=64, bits=4, scale_dtype: int = FLOAT32) -> np.ndarray:
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    sc = np.ascontiguousarray(scales, dtype=_store_np(scale_dtype))
+    bi = np.ascontiguousarray(biases, dtype=_store_np(scale_dtype))
+    rows = wq.shape[0]
+    cols = wq.shape[1] * 32 // bits
+    out = np.empty((rows, cols), dtype=np.float32)
+    rc = lib().sdo_dequantize(_p(wq), _p(sc), _p(bi), scale_dtype, rows, cols, group_size, bits, _p(out))
+    if rc != 0:
+        raise ValueError("oracle dequantize rejected its arguments")
+    return out
+
+
+def _mm_args(x, wq, scales, biases, bits):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    bi = np.ascontiguousarray(biases, dtype=np.float32)
+    M, K = x.shape
+    N = wq.shape[0]
+    assert wq.shape[1] * 32 // bits == K
+    return x, wq, sc, bi, M, N, K
+
+
+def qmatmul(x, wq, scales, biases, group_size=64, bits=4) -> np.ndarray:
+    x, wq, sc, bi, M, N, K = _mm_args(x, wq, scales, biases, bits)
+    y = np.empty((M, N), dtype=np.float32)
+    if lib().sdo_qmatmul(_p(x), M, K, _p(wq), _p(sc), _p(bi), N, group_size, bits, _p(y)) != 0:
+        raise ValueError("oracle qmatmul rejected its arguments")
+    return y
+
+
+def qmatmul_f64(x, wq, scales, biases, group_size=64, bits=4) -> np.ndarray:
+    x, wq, sc, bi, M, N, K = _mm_args(x, wq, scales, biases, bits)
+    y = np.empty((M, N), dtype=np.float64)
+    if lib().sdo_qmatmul_f64(_p(x), M, K, _p(wq), _p(sc), _p(bi), N, group_size, bits, _p(y)) != 0:
+        raise ValueError("oracle qmatmul_f64 rejected its arguments")
+    return y
+
+
+def qmatmul_omp(x, wq, scales, biases, group_size=64, bits=4, threads: int = 0) -> np.ndarray:
+    x, wq, sc, bi, M, N, K = _mm_args(x, wq, scales, biases, bits)
+    y = np.empty((M, N), dtype=np.float32)
+    t = threads or (os.cpu_count() or 1)
+    if lib().sdo_qmatmul_omp(_p(x), M, K, _p(wq), _p(sc), _p(bi), N, group_size, bits, _p(y), t) != 0:
+        raise ValueError("oracle qmatmul_omp rejected its arguments")
+    return y
+
+
+def resident_bytes(rows: int, cols: int, group_size: int = 64, bits: int = 4) -> int:
+    return int(lib().sdo_resident_bytes(rows, cols, group_size, bits))
+
+
+def gelu_approx(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().sdo_gelu_approx(_p(x), _p(y), x.size)
+    return y
+
+
+def bf16_from_f32(v: float) -> int:
+    return lib().sdo_bf16_from_f32(v)
+
+
+def f32_from_bf16(h: int) -> float:
+    return lib().sdo_f32_from_bf16(h)
+
+
+def f16_from_f32(v: float) -> int:
+    return lib().sdo_f16_from_f32(v)
+
+
+def f32_from_f16(h: int) -> float:
+    return lib().sdo_f32_from_f16(h)

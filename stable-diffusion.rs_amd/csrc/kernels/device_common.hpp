@@ -1,0 +1,109 @@
+// device_common.hpp -- element types, conversions and vector types shared by
+// the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sdq.h"
+
+namespace sdq {
+namespace dev {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// Round to nearest even (hardware v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, uint16_t(h)));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Two f32 values packed as a bf16 pair (first in the low half).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+}
+
+// Storage type and conversions per dtype code (positions of mlx_dtype).
+template <int DT> struct Elem;
+
+template <> struct Elem<SDQ_FLOAT32> {
+  using T = float;
+  static __device__ __forceinline__ float load(T v) { return v; }
+  static __device__ __forceinline__ T store(float f) { return f; }
+  static __device__ __forceinline__ float round(float f) { return f; }
+};
+
+template <> struct Elem<SDQ_BFLOAT16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T v) { return bf16_bits_to_f32(v); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_bf16_bits(f); }
+  static __device__ __forceinline__ float round(float f) {
+    return bf16_bits_to_f32(f32_to_bf16_bits(f));
+  }
+};
+
+template <> struct Elem<SDQ_FLOAT16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T v) { return f16_bits_to_f32(v); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_f16_bits(f); }
+  static __device__ __forceinline__ float round(float f) {
+    return f16_bits_to_f32(f32_to_f16_bits(f));
+  }
+};
+
+// Eight consecutive activations as a bf16x8 MFMA operand, from any of the
+// three float dtypes.  `p` must be 16-byte aligned for 16-bit types and
+// 32-byte aligned for f32.
+template <int DT> struct Load8;
+
+template <> struct Load8<SDQ_BFLOAT16> {
+  static __device__ __forceinline__ u32x4 get(const uint16_t *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+  }
+};
+
+template <> struct Load8<SDQ_FLOAT16> {
+  static __device__ __forceinline__ u32x4 get(const uint16_t *p) {
+    u32x4 v = *reinterpret_cast<const u32x4 *>(p);
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[i] = pack_bf16x2(f16_bits_to_f32(v[i] & 0xffffu), f16_bits_to_f32(v[i] >> 16));
+    return r;
+  }
+};
+
+template <> struct Load8<SDQ_FLOAT32> {
+  static __device__ __forceinline__ u32x4 get(const float *p) {
+    floatx4 a = *reinterpret_cast<const floatx4 *>(p);
+    floatx4 b = *reinterpret_cast<const floatx4 *>(p + 4);
+    u32x4 r;
+    r[0] = pack_bf16x2(a[0], a[1]);
+    r[1] = pack_bf16x2(a[2], a[3]);
+    r[2] = pack_bf16x2(b[0], b[1]);
+    r[3] = pack_bf16x2(b[2], b[3]);
+    return r;
+  }
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+} // namespace dev
+} // namespace sdq

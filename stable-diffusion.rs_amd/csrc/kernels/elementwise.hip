@@ -1,0 +1,144 @@
+// elementwise.hip -- the few elementwise ops around the quantized linear:
+// dtype casts (mlx_astype, mlx.rs:149), the bias add after the matmul
+// (quantized.rs:314-317), the T5 gate product (t5.rs:211) and tanh-GELU
+// (Array::gelu_approx, mlx.rs:1041-1054).  All compute in f32 and round once
+// to the output dtype.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include "../sdq_internal.hpp"
+
+namespace sdq {
+namespace {
+
+using namespace dev;
+
+constexpr int kThreads = 256;
+
+int grid_for(int64_t items) {
+  int64_t blocks = (items + kThreads - 1) / kThreads;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  return int(blocks);
+}
+
+template <int A, int O>
+__global__ __launch_bounds__(kThreads) void astype_kernel(const typename Elem<A>::T *__restrict__ a,
+                                                          typename Elem<O>::T *__restrict__ out,
+                                                          int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    out[i] = Elem<O>::store(Elem<A>::load(a[i]));
+}
+
+enum class BinOp { kAdd, kMul };
+
+template <BinOp OP, int A, int B, int O>
+__global__ __launch_bounds__(kThreads) void binary_kernel(const typename Elem<A>::T *__restrict__ a,
+                                                          const typename Elem<B>::T *__restrict__ b,
+                                                          typename Elem<O>::T *__restrict__ out,
+                                                          int64_t n, int64_t b_n) {
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const float x = Elem<A>::load(a[i]);
+    const float y = Elem<B>::load(b[b_n == n ? i : i % b_n]);
+    out[i] = Elem<O>::store(OP == BinOp::kAdd ? x + y : x * y);
+  }
+}
+
+// 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), the operation order
+// of mlx.rs:1048-1053.
+template <int D>
+__global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::T *__restrict__ a,
+                                                        typename Elem<D>::T *__restrict__ out,
+                                                        int64_t n) {
+  // sqrt(2 / pi) as the reference evaluates it in f32: sqrtf(2.0f / PI_f32),
+  // one ulp below the correctly rounded constant.
+  const float c = 0.7978845238685608f;
+  const float k = 0.044715f;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const float v = Elem<D>::load(a[i]);
+    const float cubed = (v * v) * v;
+    const float inner = tanhf((v + cubed * k) * c);
+    out[i] = Elem<D>::store((v * 0.5f) * (inner + 1.0f));
+  }
+}
+
+#define SDQ_FLOAT_DISPATCH(dt, NAME, ...)                                    \
+  switch (dt) {                                                              \
+  case SDQ_FLOAT32: {                                                        \
+    constexpr int NAME = SDQ_FLOAT32;                                        \
+    __VA_ARGS__;                                                             \
+    break;                                                                   \
+  }                                                                          \
+  case SDQ_BFLOAT16: {                                                       \
+    constexpr int NAME = SDQ_BFLOAT16;                                       \
+    __VA_ARGS__;                                                             \
+    break;                                                                   \
+  }                                                                          \
+  case SDQ_FLOAT16: {                                                        \
+    constexpr int NAME = SDQ_FLOAT16;                                        \
+    __VA_ARGS__;                                                             \
+    break;                                                                   \
+  }                                                                          \
+  default:                                                                   \
+    fail("unsupported dtype");                                               \
+  }
+
+} // namespace
+
+namespace kern {
+
+void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,
+            hipStream_t stream) {
+  if (n == 0) return;
+  const int grid = grid_for(n);
+  SDQ_FLOAT_DISPATCH(a_dtype, AD, SDQ_FLOAT_DISPATCH(out_dtype, OD, {
+    astype_kernel<AD, OD><<<grid, kThreads, 0, stream>>>(
+        static_cast<const typename Elem<AD>::T *>(a),
+        static_cast<typename Elem<OD>::T *>(out), n);
+  }));
+  hip_check(hipGetLastError(), "astype launch");
+}
+
+template <BinOp OP>
+static void binary(const void *a, int a_dtype, const void *b, int b_dtype,
+                   void *out, int out_dtype, int64_t n, int64_t b_n,
+                   hipStream_t stream) {
+  if (n == 0) return;
+  if (b_n <= 0 || n % b_n != 0) fail("binary op: broadcast shape mismatch");
+  const int grid = grid_for(n);
+  SDQ_FLOAT_DISPATCH(a_dtype, AD, SDQ_FLOAT_DISPATCH(b_dtype, BD, SDQ_FLOAT_DISPATCH(out_dtype, OD, {
+    binary_kernel<OP, AD, BD, OD><<<grid, kThreads, 0, stream>>>(
+        static_cast<const typename Elem<AD>::T *>(a),
+        static_cast<const typename Elem<BD>::T *>(b),
+        static_cast<typename Elem<OD>::T *>(out), n, b_n);
+  })));
+  hip_check(hipGetLastError(), "binary launch");
+}
+
+void add(const void *a, int a_dtype, const void *b, int b_dtype, void *out,
+         int out_dtype, int64_t n, int64_t b_n, hipStream_t stream) {
+  binary<BinOp::kAdd>(a, a_dtype, b, b_dtype, out, out_dtype, n, b_n, stream);
+}
+
+void multiply(const void *a, int a_dtype, const void *b, int b_dtype,
+              void *out, int out_dtype, int64_t n, hipStream_t stream) {
+  binary<BinOp::kMul>(a, a_dtype, b, b_dtype, out, out_dtype, n, n, stream);
+}
+
+void gelu_approx(const void *a, int dtype, void *out, int64_t n,
+                 hipStream_t stream) {
+  if (n == 0) return;
+  const int grid = grid_for(n);
+  SDQ_FLOAT_DISPATCH(dtype, D, {
+    gelu_kernel<D><<<grid, kThreads, 0, stream>>>(
+        static_cast<const typename Elem<D>::T *>(a),
+        static_cast<typename Elem<D>::T *>(out), n);
+  });
+  hip_check(hipGetLastError(), "gelu launch");
+}
+
+} // namespace kern
+} // namespace sdq

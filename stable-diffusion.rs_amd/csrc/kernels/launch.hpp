@@ -1,0 +1,70 @@
+// launch.hpp -- host-side launchers of the gfx950 kernels.  Each validates
+// the shape facts its kernel's indexing assumes (the op layer has already
+// checked the user-facing contract) and throws sdq::Error on failure.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdq {
+namespace kern {
+
+// w [rows, cols] (w_dtype) -> wq [rows, cols*bits/32], scales/biases
+// [rows, cols/group_size] in w_dtype.  quant.hip.
+void quantize(const void *w, int w_dtype, int64_t rows, int64_t cols,
+              int group_size, int bits, uint32_t *wq, void *scales,
+              void *biases, hipStream_t stream);
+
+// out [rows, cols] (out_dtype) = round_T(round_T(q*s) + b), T = s_dtype.
+// quant.hip.
+void dequantize(const uint32_t *wq, const void *scales, const void *biases,
+                int s_dtype, int64_t rows, int64_t cols, int group_size,
+                int bits, void *out, int out_dtype, hipStream_t stream);
+
+// Workspace the small-M kernel uses when it splits K across blocks.  The
+// counters must be zero on entry; the kernel leaves them zero.
+struct SplitWorkspace {
+  float *partial = nullptr;     // [splits, M, N] floats
+  unsigned *counters = nullptr; // [ceil(N/32)]
+};
+
+struct QmvPlan {
+  int splits = 1;
+  int groups_per_split = 0;
+  size_t partial_floats = 0; // workspace needed (0 when splits == 1)
+  int counters = 0;
+};
+
+// y [M, N] = x [M, K] @ dequantize(w).T for M <= 32.  qmv.hip.
+QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int cus);
+void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
+         const uint32_t *w, const void *scales, const void *biases,
+         int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
+         int bits, const QmvPlan &plan, const SplitWorkspace &ws,
+         hipStream_t stream);
+
+// y [M, N] = x [M, K] @ dequantize(w).T for any M.  qmm.hip.
+void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
+         const uint32_t *w, const void *scales, const void *biases,
+         int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
+         int bits, hipStream_t stream);
+
+// Elementwise helpers (elementwise.hip).  n = element count.
+void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,
+            hipStream_t stream);
+// out = a + b; b has n elements (equal shapes) or `inner` elements broadcast
+// along the last axis of a (inner = the last dimension).
+void add(const void *a, int a_dtype, const void *b, int b_dtype, void *out,
+         int out_dtype, int64_t n, int64_t b_n, hipStream_t stream);
+void multiply(const void *a, int a_dtype, const void *b, int b_dtype,
+              void *out, int out_dtype, int64_t n, hipStream_t stream);
+void gelu_approx(const void *a, int dtype, void *out, int64_t n,
+                 hipStream_t stream);
+
+// y [M, N] = a [M, K] @ b [N, K].T, f32 accumulate; y in the promotion of
+// the two dtypes.  dense.hip.
+void matmul_nt(const void *a, int a_dtype, const void *b, int b_dtype, void *y,
+               int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+} // namespace kern
+} // namespace sdq

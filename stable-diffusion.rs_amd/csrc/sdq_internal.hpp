@@ -1,0 +1,117 @@
+// sdq_internal.hpp -- shared declarations of libsdq's host runtime.
+//
+// The runtime keeps the object model the reference's mlx-c bindings assume
+// (crates/sd-tensor/src/mlx.rs:38-98, 558-612): reference-counted arrays
+// behind opaque handles, streams as handles, a process-wide error handler,
+// and explicit evaluation.  Arrays live in HBM; their buffers come from a
+// per-device caching allocator so that steady-state calls never reach
+// hipMalloc.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "sdq.h"
+
+namespace sdq {
+
+// Every failure inside the library is thrown as this and turned into a
+// status + handler message at the C boundary.
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const std::string &msg);
+void hip_check(hipError_t e, const char *what);
+
+size_t dtype_size(int dtype);
+const char *dtype_name(int dtype);
+bool is_float_dtype(int dtype);  // float32, bfloat16, float16
+int promote_float(int a, int b); // MLX promotion among the three float types
+
+// ---- device memory ------------------------------------------------------
+
+// One device allocation.  When the last reference goes, the block returns to
+// the allocator's cache, tagged with the stream that last used it: reuse on
+// that stream is ordered by the stream; reuse on another first waits for it.
+struct Buffer {
+  void *ptr = nullptr;
+  size_t capacity = 0;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  ~Buffer();
+};
+
+std::shared_ptr<Buffer> allocate(size_t bytes, int device, hipStream_t stream);
+size_t active_memory();
+size_t peak_memory();
+size_t cache_memory();
+void reset_peak_memory();
+size_t set_cache_limit(size_t limit); // returns the previous limit
+void clear_cache();
+
+// ---- streams ------------------------------------------------------------
+
+struct StreamImpl {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool cpu = false;
+  bool owned = false; // created by sdq_gpu_stream_new, destroyed on free
+};
+
+StreamImpl *stream_of(sdq_stream s, const char *op);
+
+// ---- arrays -------------------------------------------------------------
+
+struct ArrayImpl {
+  std::vector<int> shape;
+  int dtype = SDQ_FLOAT32;
+  size_t size = 0; // elements
+  std::shared_ptr<Buffer> buf;
+  int device = 0;
+  hipStream_t stream = nullptr; // the stream whose work produces the data
+  std::vector<unsigned char> host; // mirror returned by the data accessors
+
+  size_t nbytes() const { return size * dtype_size(dtype); }
+  void *data() const { return buf ? buf->ptr : nullptr; }
+};
+
+ArrayImpl *array_of(sdq_array a, const char *op, const char *name);
+// A new device array of the given shape, allocated for `s`.
+std::unique_ptr<ArrayImpl> make_array(const std::vector<int> &shape, int dtype,
+                                      const StreamImpl &s);
+// Moves `value` into the result handle (allocating the handle when empty).
+void set_result(sdq_array *res, std::unique_ptr<ArrayImpl> value);
+// A second reference to the same data (metadata copied, buffer shared).
+ArrayImpl share(const ArrayImpl &a);
+
+struct VectorImpl {
+  std::vector<ArrayImpl> items;
+};
+// Replaces the contents of the result vector (allocating it when empty).
+void set_vector_result(sdq_vector_array *res,
+                       std::vector<std::unique_ptr<ArrayImpl>> values);
+std::string shape_str(const std::vector<int> &shape);
+
+// Reports `msg` for op `op` through the installed handler.
+void report(const char *op, const char *msg);
+
+} // namespace sdq
+
+// Wraps a C entry point body: exceptions become status 1 plus a message.
+#define SDQ_GUARD(op, ...)                                                   \
+  try {                                                                      \
+    __VA_ARGS__;                                                             \
+    return 0;                                                                \
+  } catch (const std::exception &e) {                                        \
+    ::sdq::report(op, e.what());                                             \
+    return 1;                                                                \
+  } catch (...) {                                                            \
+    ::sdq::report(op, "unknown failure");                                    \
+    return 1;                                                                \
+  }

@@ -1,0 +1,431 @@
+// sdq_ops.cpp -- the op entry points of libsdq's C ABI: quantize, dequantize,
+// quantized_matmul and the elementwise ops around them.  Each validates its
+// arguments the way the reference's callers expect MLX to (a non-zero status
+// and a message, never an abort: mlx.rs:853-863 records MLX aborting on some
+// inputs), orders its inputs on the stream, and enqueues HIP kernels.
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "kernels/launch.hpp"
+#include "sdq_internal.hpp"
+
+namespace sdq {
+namespace {
+
+// Waits on `s` for the work that produced `a`, when that ran elsewhere.
+void order_after(const ArrayImpl *a, const StreamImpl *s) {
+  if (!a->stream || a->stream == s->stream) return;
+  hipEvent_t ev;
+  hip_check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate");
+  hip_check(hipEventRecord(ev, a->stream), "hipEventRecord");
+  hip_check(hipStreamWaitEvent(s->stream, ev, 0), "hipStreamWaitEvent");
+  hip_check(hipEventDestroy(ev), "hipEventDestroy");
+}
+
+void same_device(const ArrayImpl *a, const StreamImpl *s, const char *name) {
+  if (a->device != s->device)
+    fail(std::string("`") + name + "` lives on device " + std::to_string(a->device) +
+         " but the stream is on device " + std::to_string(s->device));
+}
+
+int opt_or(sdq_optional_int v, int dflt) { return v.has_value ? v.value : dflt; }
+
+void check_mode(const char *mode, sdq_array global_scale) {
+  if (mode && std::strcmp(mode, "affine") != 0)
+    fail(std::string("Invalid quantization mode '") + mode +
+         "'; libsdq implements 'affine' (scale and bias per group)");
+  if (global_scale.ctx)
+    fail("global_scale applies to the nvfp4 mode only and must be empty for 'affine'");
+}
+
+void check_group_bits(int gs, int bits) {
+  if (gs != 32 && gs != 64 && gs != 128)
+    fail("The requested group size " + std::to_string(gs) +
+         " is not supported. The supported group sizes are 32, 64 and 128.");
+  if (bits != 2 && bits != 4 && bits != 8)
+    fail("The requested number of bits " + std::to_string(bits) +
+         " is not supported. The supported bits are 2, 4 and 8.");
+}
+
+int cu_count(int device) {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(device);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device),
+            "hipDeviceGetAttribute");
+  cache[device] = n;
+  return n;
+}
+
+// Per-stream split-K counters: zeroed once when (re)allocated; every kernel
+// that uses them leaves them zero again.
+unsigned *split_counters(int device, hipStream_t stream, int needed) {
+  struct Slot {
+    std::shared_ptr<Buffer> buf;
+    int count = 0;
+  };
+  static std::mutex mu;
+  static std::map<hipStream_t, Slot> slots;
+  std::lock_guard<std::mutex> lock(mu);
+  Slot &slot = slots[stream];
+  if (slot.count < needed) {
+    const int count = std::max(needed, 4096);
+    auto buf = allocate(size_t(count) * sizeof(unsigned), device, stream);
+    hip_check(hipMemsetAsync(buf->ptr, 0, size_t(count) * sizeof(unsigned), stream),
+              "hipMemsetAsync");
+    slot.buf = buf;
+    slot.count = count;
+  }
+  return static_cast<unsigned *>(slot.buf->ptr);
+}
+
+// y = x @ dequantize(w).T on device pointers; picks the kernel by M.
+void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
+                     const uint32_t *w, const void *scales, const void *biases,
+                     int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
+                     int device, hipStream_t stream,
+                     std::shared_ptr<Buffer> *keep_alive) {
+  if (M == 0 || N == 0) return;
+  if (gs != 64 && gs != 128)
+    fail("the quantized matmul kernels take group size 64 or 128, got " + std::to_string(gs));
+  if (bits != 4 && bits != 8)
+    fail("the quantized matmul kernels take 4 or 8 bits, got " + std::to_string(bits));
+  if (M <= 32) {
+    kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, cu_count(device));
+    kern::SplitWorkspace ws;
+    if (plan.splits > 1) {
+      *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
+      ws.partial = static_cast<float *>((*keep_alive)->ptr);
+      ws.counters = split_counters(device, stream, plan.counters);
+    }
+    kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
+              plan, ws, stream);
+  } else {
+    kern::qmm(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
+              stream);
+  }
+}
+
+} // namespace
+} // namespace sdq
+
+using namespace sdq;
+
+extern "C" {
+
+int sdq_quantize(sdq_vector_array *res, sdq_array w, sdq_optional_int group_size,
+                 sdq_optional_int bits, const char *mode, sdq_array global_scale,
+                 sdq_stream s) {
+  SDQ_GUARD("quantize", {
+    StreamImpl *st = stream_of(s, "quantize");
+    if (!res) fail("result pointer is NULL");
+    check_mode(mode, global_scale);
+    const int gs = opt_or(group_size, 64);
+    const int nb = opt_or(bits, 4);
+    check_group_bits(gs, nb);
+    ArrayImpl *wa = array_of(w, "quantize", "w");
+    same_device(wa, st, "w");
+    if (wa->shape.size() < 2)
+      fail("The matrix to be quantized must have at least 2 dimensions but it has only " +
+           std::to_string(wa->shape.size()) + ".");
+    if (!is_float_dtype(wa->dtype))
+      fail(std::string("Only float32, bfloat16 and float16 matrices can be quantized, got ") +
+           dtype_name(wa->dtype));
+    const int K = wa->shape.back();
+    if (K % gs != 0)
+      fail("The last dimension of the matrix needs to be divisible by the quantization "
+           "group size " +
+           std::to_string(gs) + ". However the provided matrix has shape " +
+           shape_str(wa->shape));
+    order_after(wa, st);
+    std::vector<int> qshape = wa->shape, sshape = wa->shape;
+    qshape.back() = int(int64_t(K) * nb / 32);
+    sshape.back() = K / gs;
+    auto wq = make_array(qshape, SDQ_UINT32, *st);
+    auto sc = make_array(sshape, wa->dtype, *st);
+    auto bi = make_array(sshape, wa->dtype, *st);
+    const int64_t rows = K ? int64_t(wa->size / size_t(K)) : 0;
+    kern::quantize(wa->data(), wa->dtype, rows, K, gs, nb,
+                   static_cast<uint32_t *>(wq->data()), sc->data(), bi->data(), st->stream);
+    std::vector<std::unique_ptr<ArrayImpl>> parts;
+    parts.push_back(std::move(wq));
+    parts.push_back(std::move(sc));
+    parts.push_back(std::move(bi));
+    set_vector_result(res, std::move(parts));
+  });
+}
+
+int sdq_dequantize(sdq_array *res, sdq_array w, sdq_array scales, sdq_array biases,
+                   sdq_optional_int group_size, sdq_optional_int bits, const char *mode,
+                   sdq_array global_scale, sdq_optional_dtype dtype, sdq_stream s) {
+  SDQ_GUARD("dequantize", {
+    StreamImpl *st = stream_of(s, "dequantize");
+    check_mode(mode, global_scale);
+    const int gs = opt_or(group_size, 64);
+    const int nb = opt_or(bits, 4);
+    check_group_bits(gs, nb);
+    ArrayImpl *wa = array_of(w, "dequantize", "w");
+    ArrayImpl *sa = array_of(scales, "dequantize", "scales");
+    ArrayImpl *ba = array_of(biases, "dequantize", "biases");
+    same_device(wa, st, "w");
+    same_device(sa, st, "scales");
+    same_device(ba, st, "biases");
+    if (wa->dtype != SDQ_UINT32)
+      fail(std::string("The matrix should be given as a uint32, got ") + dtype_name(wa->dtype));
+    if (wa->shape.size() < 2)
+      fail("The matrix to be dequantized must have at least 2 dimensions");
+    if (sa->shape != ba->shape || sa->dtype != ba->dtype)
+      fail("Shape and dtype of scales and biases should match: " + shape_str(sa->shape) + " " +
+           dtype_name(sa->dtype) + " vs " + shape_str(ba->shape) + " " + dtype_name(ba->dtype));
+    if (!is_float_dtype(sa->dtype))
+      fail(std::string("scales must be float32, bfloat16 or float16, got ") + dtype_name(sa->dtype));
+    const int64_t K = int64_t(wa->shape.back()) * 32 / nb;
+    std::vector<int> lead_w(wa->shape.begin(), wa->shape.end() - 1);
+    std::vector<int> lead_s(sa->shape.begin(), sa->shape.end() - 1);
+    if (lead_w != lead_s || int64_t(sa->shape.back()) * gs != K)
+      fail("Shape of scales and biases does not match the matrix given the quantization "
+           "parameters. Provided matrix of shape " +
+           shape_str(wa->shape) + " and scales/biases of shape " + shape_str(sa->shape) +
+           " with group_size=" + std::to_string(gs) + " and bits=" + std::to_string(nb) + ".");
+    int out_dtype = sa->dtype;
+    if (dtype.has_value) {
+      if (!is_float_dtype(dtype.value))
+        fail(std::string("dtype must be float32, bfloat16 or float16, got ") + dtype_name(dtype.value));
+      out_dtype = dtype.value;
+    }
+    order_after(wa, st);
+    order_after(sa, st);
+    order_after(ba, st);
+    std::vector<int> oshape = wa->shape;
+    oshape.back() = int(K);
+    auto out = make_array(oshape, out_dtype, *st);
+    const int64_t rows = K ? int64_t(out->size / size_t(K)) : 0;
+    kern::dequantize(static_cast<const uint32_t *>(wa->data()), sa->data(), ba->data(), sa->dtype,
+                     rows, K, gs, nb, out->data(), out_dtype, st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                         sdq_array biases, bool transpose, sdq_optional_int group_size,
+                         sdq_optional_int bits, const char *mode, sdq_stream s) {
+  SDQ_GUARD("quantized_matmul", {
+    StreamImpl *st = stream_of(s, "quantized_matmul");
+    check_mode(mode, sdq_array{nullptr});
+    const int gs = opt_or(group_size, 64);
+    const int nb = opt_or(bits, 4);
+    check_group_bits(gs, nb);
+    if (!transpose)
+      fail("transpose=false (x @ W with W quantized along its output axis) is not "
+           "implemented; the diffusers [out, in] layout uses transpose=true");
+    ArrayImpl *xa = array_of(x, "quantized_matmul", "x");
+    ArrayImpl *wa = array_of(w, "quantized_matmul", "w");
+    ArrayImpl *sa = array_of(scales, "quantized_matmul", "scales");
+    ArrayImpl *ba = array_of(biases, "quantized_matmul", "biases");
+    same_device(xa, st, "x");
+    same_device(wa, st, "w");
+    same_device(sa, st, "scales");
+    same_device(ba, st, "biases");
+    if (wa->dtype != SDQ_UINT32)
+      fail(std::string("The weight matrix should be uint32, got ") + dtype_name(wa->dtype));
+    if (wa->shape.size() != 2)
+      fail("The weight matrix must be 2-D [out, in*bits/32], got shape " + shape_str(wa->shape));
+    if (!is_float_dtype(xa->dtype))
+      fail(std::string("x must be float32, bfloat16 or float16, got ") + dtype_name(xa->dtype));
+    if (sa->shape != ba->shape || sa->dtype != ba->dtype || !is_float_dtype(sa->dtype))
+      fail("scales and biases must share one float dtype and one shape, got " +
+           shape_str(sa->shape) + " " + dtype_name(sa->dtype) + " and " + shape_str(ba->shape) +
+           " " + dtype_name(ba->dtype));
+    const int64_t N = wa->shape[0];
+    const int64_t K = int64_t(wa->shape[1]) * 32 / nb;
+    if (sa->shape.size() != 2 || sa->shape[0] != N || int64_t(sa->shape[1]) * gs != K)
+      fail("Shape of scales and biases does not match the matrix given the quantization "
+           "parameters. Provided matrix of shape " +
+           shape_str(wa->shape) + " and scales/biases of shape " + shape_str(sa->shape) +
+           " with group_size=" + std::to_string(gs) + " and bits=" + std::to_string(nb) + ".");
+    if (xa->shape.empty() || xa->shape.back() != K)
+      fail("Last dimension of first input with shape " + shape_str(xa->shape) +
+           " must match the dequantized weight's input width " + std::to_string(K) +
+           " (weight " + shape_str(wa->shape) + ", bits=" + std::to_string(nb) + ")");
+    const int out_dtype = promote_float(xa->dtype, sa->dtype);
+    order_after(xa, st);
+    order_after(wa, st);
+    order_after(sa, st);
+    order_after(ba, st);
+    std::vector<int> oshape = xa->shape;
+    oshape.back() = int(N);
+    auto out = make_array(oshape, out_dtype, *st);
+    const int64_t M = K ? int64_t(xa->size / size_t(K)) : 0;
+    std::shared_ptr<Buffer> scratch;
+    matmul_dispatch(out->data(), out_dtype, xa->data(), xa->dtype, K,
+                    static_cast<const uint32_t *>(wa->data()), sa->data(), ba->data(), sa->dtype,
+                    M, N, K, gs, nb, st->device, st->stream, &scratch);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
+                             const uint32_t *w, const void *scales, const void *biases,
+                             int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
+                             int bits, void *hip_stream) {
+  SDQ_GUARD("quantized_matmul_raw", {
+    if (M < 0 || N < 0 || K <= 0) fail("M, N must be >= 0 and K > 0");
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(s_dtype) || !is_float_dtype(y_dtype))
+      fail("dtypes must be float32, bfloat16 or float16");
+    check_group_bits(group_size, bits);
+    if (K % group_size != 0) fail("K must be a multiple of group_size");
+    if (M > 0 && N > 0 && (!y || !x || !w || !scales || !biases)) fail("NULL pointer argument");
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    std::shared_ptr<Buffer> scratch;
+    matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch);
+  });
+}
+
+int sdq_gelu_approx_raw(void *out, const void *in, int dtype, int64_t n, void *hip_stream) {
+  SDQ_GUARD("gelu_approx_raw", {
+    if (!is_float_dtype(dtype)) fail("dtype must be float32, bfloat16 or float16");
+    if (n < 0) fail("negative element count");
+    if (n > 0 && (!out || !in)) fail("NULL pointer argument");
+    kern::gelu_approx(in, dtype, out, n, static_cast<hipStream_t>(hip_stream));
+  });
+}
+
+void *sdq_array_device_ptr(sdq_array arr) {
+  auto *a = static_cast<ArrayImpl *>(arr.ctx);
+  return a ? a->data() : nullptr;
+}
+
+int sdq_add(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s) {
+  SDQ_GUARD("add", {
+    StreamImpl *st = stream_of(s, "add");
+    ArrayImpl *aa = array_of(a, "add", "a");
+    ArrayImpl *bb = array_of(b, "add", "b");
+    same_device(aa, st, "a");
+    same_device(bb, st, "b");
+    if (!is_float_dtype(aa->dtype) || !is_float_dtype(bb->dtype))
+      fail("add takes float32, bfloat16 or float16 arrays");
+    const bool same = aa->shape == bb->shape;
+    const bool bias = bb->shape.size() == 1 && !aa->shape.empty() &&
+                      bb->shape[0] == aa->shape.back();
+    if (!same && !bias)
+      fail("Shapes " + shape_str(aa->shape) + " and " + shape_str(bb->shape) +
+           " cannot be broadcast (libsdq adds equal shapes or a bias along the last axis)");
+    order_after(aa, st);
+    order_after(bb, st);
+    const int od = promote_float(aa->dtype, bb->dtype);
+    auto out = make_array(aa->shape, od, *st);
+    kern::add(aa->data(), aa->dtype, bb->data(), bb->dtype, out->data(), od,
+              int64_t(aa->size), int64_t(bb->size), st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_multiply(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s) {
+  SDQ_GUARD("multiply", {
+    StreamImpl *st = stream_of(s, "multiply");
+    ArrayImpl *aa = array_of(a, "multiply", "a");
+    ArrayImpl *bb = array_of(b, "multiply", "b");
+    same_device(aa, st, "a");
+    same_device(bb, st, "b");
+    if (!is_float_dtype(aa->dtype) || !is_float_dtype(bb->dtype))
+      fail("multiply takes float32, bfloat16 or float16 arrays");
+    if (aa->shape != bb->shape)
+      fail("Shapes " + shape_str(aa->shape) + " and " + shape_str(bb->shape) +
+           " must be equal");
+    order_after(aa, st);
+    order_after(bb, st);
+    const int od = promote_float(aa->dtype, bb->dtype);
+    auto out = make_array(aa->shape, od, *st);
+    kern::multiply(aa->data(), aa->dtype, bb->data(), bb->dtype, out->data(), od,
+                   int64_t(aa->size), st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_astype(sdq_array *res, sdq_array a, sdq_dtype dtype, sdq_stream s) {
+  SDQ_GUARD("astype", {
+    StreamImpl *st = stream_of(s, "astype");
+    ArrayImpl *aa = array_of(a, "astype", "a");
+    same_device(aa, st, "a");
+    order_after(aa, st);
+    auto out = make_array(aa->shape, dtype, *st);
+    if (aa->dtype == int(dtype)) {
+      if (out->nbytes())
+        hip_check(hipMemcpyAsync(out->data(), aa->data(), out->nbytes(),
+                                 hipMemcpyDeviceToDevice, st->stream),
+                  "hipMemcpyAsync");
+    } else {
+      if (!is_float_dtype(aa->dtype) || !is_float_dtype(dtype))
+        fail(std::string("astype converts between float32, bfloat16 and float16, not ") +
+             dtype_name(aa->dtype) + " -> " + dtype_name(dtype));
+      kern::astype(aa->data(), aa->dtype, out->data(), dtype, int64_t(aa->size), st->stream);
+    }
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_contiguous(sdq_array *res, sdq_array a, bool allow_col_major, sdq_stream s) {
+  (void)allow_col_major;
+  SDQ_GUARD("contiguous", {
+    StreamImpl *st = stream_of(s, "contiguous");
+    ArrayImpl *aa = array_of(a, "contiguous", "a");
+    same_device(aa, st, "a");
+    order_after(aa, st);
+    auto out = make_array(aa->shape, aa->dtype, *st);
+    if (out->nbytes())
+      hip_check(hipMemcpyAsync(out->data(), aa->data(), out->nbytes(), hipMemcpyDeviceToDevice,
+                               st->stream),
+                "hipMemcpyAsync");
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_matmul_nt(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s) {
+  SDQ_GUARD("matmul", {
+    StreamImpl *st = stream_of(s, "matmul");
+    ArrayImpl *aa = array_of(a, "matmul", "a");
+    ArrayImpl *bb = array_of(b, "matmul", "b");
+    same_device(aa, st, "a");
+    same_device(bb, st, "b");
+    if (!is_float_dtype(aa->dtype) || !is_float_dtype(bb->dtype))
+      fail("matmul takes float32, bfloat16 or float16 arrays");
+    if (bb->shape.size() != 2 || aa->shape.empty() || aa->shape.back() != bb->shape[1])
+      fail("Shapes " + shape_str(aa->shape) + " and " + shape_str(bb->shape) +
+           " do not contract: a is [..., K] and b is [N, K]");
+    order_after(aa, st);
+    order_after(bb, st);
+    const int64_t K = bb->shape[1];
+    const int64_t N = bb->shape[0];
+    std::vector<int> oshape = aa->shape;
+    oshape.back() = int(N);
+    const int od = promote_float(aa->dtype, bb->dtype);
+    auto out = make_array(oshape, od, *st);
+    const int64_t M = K ? int64_t(aa->size / size_t(K)) : 0;
+    if (K == 0) fail("matmul over an empty contraction axis");
+    kern::matmul_nt(aa->data(), aa->dtype, bb->data(), bb->dtype, out->data(), M, N, K,
+                    st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_gelu_approx(sdq_array *res, sdq_array a, sdq_stream s) {
+  SDQ_GUARD("gelu_approx", {
+    StreamImpl *st = stream_of(s, "gelu_approx");
+    ArrayImpl *aa = array_of(a, "gelu_approx", "a");
+    same_device(aa, st, "a");
+    if (!is_float_dtype(aa->dtype)) fail("gelu_approx takes a float array");
+    order_after(aa, st);
+    auto out = make_array(aa->shape, aa->dtype, *st);
+    kern::gelu_approx(aa->data(), aa->dtype, out->data(), int64_t(aa->size), st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+} // extern "C"

@@ -1,0 +1,175 @@
+"""GPU quantized_matmul through the C ABI against the oracle (the north
+star's second parity level): max relative error <= 2e-2 (max |d| / max |ref|)
+and cosine >= 0.9999 against the f64 product of the oracle's dequantized
+weight, on the same seeded inputs.  Covers both kernels (M <= 32: the
+bandwidth kernel; M > 32: the MFMA tile kernel), tails in M and N, split-K,
+dtype promotion, group size 128, and the BASELINE shapes at full size."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import cosine, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 2e-2
+MIN_COS = 0.9999
+XDT = {"f32": 10, "bf16": 12, "f16": 9}
+
+
+def _x(oracle, sdq, seed, shape, xdt):
+    x = oracle.normals(seed, int(np.prod(shape))).reshape(shape)
+    if xdt == "bf16":
+        bits = sdq.f32_to_bf16_bits(x)
+        return sdq.Array.from_numpy(bits, sdq.BFLOAT16), sdq.bf16_bits_to_f32(bits).reshape(shape)
+    if xdt == "f16":
+        h = x.astype(np.float16)
+        return sdq.Array.from_numpy(h, sdq.FLOAT16), h.astype(np.float32)
+    return sdq.Array.from_numpy(x, sdq.FLOAT32), x
+
+
+def _qweight(oracle, sdq, stream, seed, N, K, bits, gs=64, sdt="f32"):
+    w = oracle.normals(seed, N * K, 0.02).reshape(N, K)
+    if sdt == "bf16":
+        wb = sdq.f32_to_bf16_bits(w)
+        w_dev = sdq.Array.from_numpy(wb, sdq.BFLOAT16)
+        w = sdq.bf16_bits_to_f32(wb).reshape(N, K)
+    else:
+        w_dev = sdq.Array.from_numpy(w)
+    q = sdq.QuantizedArray.quantize(w_dev, gs, bits, stream)
+    s_code = 12 if sdt == "bf16" else 10
+    wq, s, b = oracle.quantize(w, gs, bits, s_code)
+    deq = oracle.dequantize(wq, s, b, gs, bits, s_code)
+    return q, deq
+
+
+def _check(got, x_vals, deq):
+    want = x_vals.reshape(-1, x_vals.shape[-1]).astype(np.float64) @ deq.astype(np.float64).T
+    got = got.reshape(want.shape)
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
+    return err, cos
+
+
+CASES = [
+    # (M, N, K, bits) -- M <= 32 is the bandwidth kernel, above is the MFMA tile kernel
+    (1, 256, 512, 4), (1, 100, 512, 8), (2, 96, 256, 4), (3, 64, 64, 4), (4, 320, 1024, 8),
+    (7, 256, 192, 4), (15, 128, 512, 8), (16, 256, 512, 4), (17, 200, 256, 4), (31, 64, 512, 8),
+    (32, 288, 384, 4), (33, 256, 512, 4), (48, 300, 256, 8), (64, 512, 256, 4), (100, 96, 128, 8),
+    (128, 256, 512, 4), (129, 320, 256, 4), (255, 256, 192, 8), (256, 512, 512, 4),
+    (257, 64, 128, 4), (300, 500, 320, 8), (513, 1024, 256, 4),
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits", CASES)
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_quantized_matmul_matches_the_oracle(oracle, sdq, stream, M, N, K, bits, xdt):
+    print(f"qmatmul M={M} N={N} K={K} bits={bits} x={xdt}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 400 + N + K + bits, N, K, bits)
+    x_dev, x_vals = _x(oracle, sdq, 500 + M, (M, K), xdt)
+    y = q.matmul(x_dev, stream)
+    assert y.shape == [M, N]
+    assert y.dtype == sdq.FLOAT32  # promote(x, f32 scales) = f32
+    _check(y.to_numpy(), x_vals, deq)
+
+
+@pytest.mark.parametrize("M", [1, 16, 200])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_bf16_scales_give_bf16_output(oracle, sdq, stream, M, bits):
+    print(f"bf16 scales M={M} bits={bits}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 600 + M, 192, 256, bits, sdt="bf16")
+    x_dev, x_vals = _x(oracle, sdq, 601 + M, (M, 256), "bf16")
+    y = q.matmul(x_dev, stream)
+    assert y.dtype == sdq.BFLOAT16
+    _check(sdq.bf16_bits_to_f32(y.to_numpy()), x_vals, deq)
+
+
+@pytest.mark.parametrize("M", [1, 9, 77])
+def test_group_size_128(oracle, sdq, stream, M):
+    print(f"gs128 M={M}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 700 + M, 160, 512, 4, gs=128)
+    x_dev, x_vals = _x(oracle, sdq, 701 + M, (M, 512), "bf16")
+    _check(q.matmul(x_dev, stream).to_numpy(), x_vals, deq)
+
+
+@pytest.mark.parametrize("xdt", ["f16"])
+@pytest.mark.parametrize("M", [5, 70])
+def test_f16_activations(oracle, sdq, stream, xdt, M):
+    q, deq = _qweight(oracle, sdq, stream, 750 + M, 128, 256, 8)
+    x_dev, x_vals = _x(oracle, sdq, 751 + M, (M, 256), xdt)
+    _check(q.matmul(x_dev, stream).to_numpy(), x_vals, deq)
+
+
+def test_leading_dimensions_of_x(oracle, sdq, stream):
+    # Flux feeds [1, seq, K] token tensors (flux.rs:352-357).
+    q, deq = _qweight(oracle, sdq, stream, 800, 96, 128, 4)
+    x_dev, x_vals = _x(oracle, sdq, 801, (1, 40, 128), "bf16")
+    y = q.matmul(x_dev, stream)
+    assert y.shape == [1, 40, 96]
+    _check(y.to_numpy(), x_vals, deq)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 32])
+def test_split_k_is_deterministic_and_correct(oracle, sdq, stream, M):
+    # Few 32-row tiles and a long K force the K split across blocks; the
+    # last block sums the partials in split order, so repeated calls agree
+    # bit for bit and the per-tile counters are left ready for the next call.
+    print(f"split-K M={M}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 900 + M, 64, 8192, 4)
+    x_dev, x_vals = _x(oracle, sdq, 901 + M, (M, 8192), "bf16")
+    first = q.matmul(x_dev, stream).to_numpy()
+    _check(first, x_vals, deq)
+    for _ in range(3):
+        assert np.array_equal(q.matmul(x_dev, stream).to_numpy(), first)
+
+
+def test_repeated_calls_are_identical(oracle, sdq, stream):
+    q, _ = _qweight(oracle, sdq, stream, 950, 512, 1024, 8)
+    x_dev, _ = _x(oracle, sdq, 951, (300, 1024), "bf16")
+    a = q.matmul(x_dev, stream).to_numpy()
+    b = q.matmul(x_dev, stream).to_numpy()
+    assert np.array_equal(a, b)
+
+
+def test_small_m_kernel_is_near_exact(oracle, sdq, stream):
+    # The bandwidth kernel applies scale and bias once per group to exact
+    # integer-code products, so it tracks the f64 reference to ~1e-6.
+    q, deq = _qweight(oracle, sdq, stream, 960, 256, 2048, 4)
+    x_dev, x_vals = _x(oracle, sdq, 961, (8, 2048), "bf16")
+    err, _ = _check(q.matmul(x_dev, stream).to_numpy(), x_vals, deq)
+    assert err < 1e-5
+
+
+# ---- BASELINE shapes at full size -------------------------------------------------
+
+
+def _sampled_check(oracle, sdq, stream, M, N, K, bits, seed, rows=48):
+    print(f"full-size M={M} N={N} K={K} bits={bits}", flush=True)
+    w = oracle.normals(seed, N * K, 0.02).reshape(N, K)
+    q = sdq.QuantizedArray.quantize(sdq.Array.from_numpy(w), 64, bits, stream)
+    wq, s, b = oracle.quantize(w, 64, bits)
+    # Quantization itself is bit-exact at full size too.
+    assert np.array_equal(q.weight.to_numpy(), wq)
+    deq = oracle.dequantize(wq, s, b, 64, bits)
+    x_dev, x_vals = _x(oracle, sdq, seed + 1, (M, K), "bf16")
+    y = q.matmul(x_dev, stream).to_numpy()
+    pick = np.unique(np.linspace(0, M - 1, min(rows, M)).astype(int))
+    _check(y[pick], x_vals[pick], deq)
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("M,N,K,bits", [
+    (1536, 12288, 3072, 4),   # config 2: Flux fc1
+    (1536, 3072, 12288, 8),   # config 2: Flux fc2
+    (512, 10240, 4096, 4),    # config 3: T5 wi_0 / wi_1
+    (16, 4096, 10240, 8),     # config 3: T5 wo, M = 16
+    (1, 10240, 4096, 4),      # config 3: T5 wi, M = 1
+    (4608, 21504, 3072, 4),   # config 4: Flux linear1
+    (4608, 3072, 15360, 8),   # config 4: Flux linear2
+    (1, 9216, 3072, 8),       # config 4: adaLN modulation
+    (4096, 64, 3072, 8),      # config 5: final_layer.linear (N = 64)
+    (4096, 3072, 64, 8),      # config 5: img_in (K = 64, one group)
+])
+def test_baseline_shapes(oracle, sdq, stream, M, N, K, bits):
+    _sampled_check(oracle, sdq, stream, M, N, K, bits, seed=1000 + M + N + K)
