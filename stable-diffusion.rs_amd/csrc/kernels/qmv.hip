@@ -118,8 +118,12 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(
       for (int c = 0; c < 8; ++c) {
         const u32x4 v = Load8<XDT>::get(src + 8 * c);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v[j]), ones, sum, false);
+        for (int j = 0; j < 4; ++j) {
+          // Copy the element out first: bit-casting a vector-element
+          // expression directly reinterprets element 0 instead.
+          const uint32_t pair = v[j];
+          sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), ones, sum, false);
+        }
       }
       xsum[sl * MROWS + m] = sum;
     }

@@ -26,7 +26,8 @@ def _weights(oracle, sdq, seed, shape, wdt):
 
 def _raw(a):
     """Device scales/biases as the oracle stores them (f32, or uint16 bits)."""
-    return a.to_numpy()
+    v = a.to_numpy()
+    return v.view(np.uint16) if v.dtype == np.float16 else v
 
 
 @pytest.mark.parametrize("wdt", ["f32", "bf16", "f16"])
