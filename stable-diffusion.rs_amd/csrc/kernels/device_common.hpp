@@ -33,9 +33,22 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
-// Two f32 values packed as a bf16 pair (first in the low half).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// Two f32 values packed as a bf16 pair (first in the low half), rounded to
+// nearest even: one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+  const floatx2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// Hides a value's known bits from the optimizer (no instruction is emitted),
+// so that byte-field conversions select v_cvt_f32_ubyte{0..3} directly
+// instead of re-extracting fields it believes are narrower.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
 }
 
 // Storage type and conversions per dtype code (positions of mlx_dtype).

@@ -42,8 +42,8 @@ __device__ __forceinline__ u32x4 dequant8(const u32x4 (&wr)[BITS / 4], int i, fl
 template <>
 __device__ __forceinline__ u32x4 dequant8<4>(const u32x4 (&wr)[1], int i, float s, float b) {
   const uint32_t wd = wr[0][i];
-  const uint32_t lo = wd & 0x0F0F0F0Fu;        // codes 0, 2, 4, 6
-  const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu; // codes 1, 3, 5, 7
+  const uint32_t lo = opaque(wd & 0x0F0F0F0Fu);        // codes 0, 2, 4, 6
+  const uint32_t hi = opaque((wd >> 4) & 0x0F0F0F0Fu); // codes 1, 3, 5, 7
   u32x4 r;
 #pragma unroll
   for (int d = 0; d < 4; ++d)
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
 #pragma unroll
     for (int q = 0; q < MB; ++q) {
       const int row = sr + 32 * q;
-      *reinterpret_cast<u32x4 *>(&xs[buf][row * 32 + ((sc ^ (row & 7)) * 4)]) = xr[q];
+      *reinterpret_cast<u32x4 *>(&xs[buf][row * 32 + ((sc ^ ((row >> 1) & 7)) * 4)]) = xr[q];
     }
   };
   auto load_w = [&](int step, u32x4 (&wr)[2][kWV], float (&s)[2], float (&b)[2]) {
@@ -152,36 +152,78 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
 
   for (int step = 0; step < steps; ++step) {
     const int buf = step & 1;
-    const bool more = step + 1 < steps;
+    // The next step's loads are issued unconditionally (the last iteration
+    // reloads its own step into the idle buffer), so the loop body has no
+    // branch and each wait counts only the loads it needs.
+    const int next = step + 1 < steps ? step + 1 : step;
     u32x4 xr[MB];
     u32x4 wn[2][kWV];
     float sn[2], bn[2];
-    if (more) {
-      stage_load(step + 1, xr);
-      load_w(step + 1, wn, sn, bn);
-    }
+    stage_load(next, xr);
+    load_w(next, wn, sn, bn);
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t *xb = xs[buf];
+    // Operand fragments are double-buffered across the four k-steps: the
+    // LDS reads and the dequantization of k-step i + 1 are issued before the
+    // MFMAs of k-step i, so their latency hides under the matrix work.
+    u32x4 a[2][MB];
+    u32x4 bq[2][2];
+    auto read_a = [&](int i, u32x4 (&dst)[MB]) {
+      const int chunk = (4 * h + i) ^ ((r >> 1) & 7);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        dst[mb] = *reinterpret_cast<const u32x4 *>(&xb[(mb * 32 + r) * 32 + chunk * 4]);
+    };
+    read_a(0, a[0]);
+    bq[0][0] = dequant8<BITS>(wc[0], 0, scur[0], bcur[0]);
+    bq[0][1] = dequant8<BITS>(wc[1], 0, scur[1], bcur[1]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x4 b0 = dequant8<BITS>(wc[0], i, scur[0], bcur[0]);
-      const u32x4 b1 = dequant8<BITS>(wc[1], i, scur[1], bcur[1]);
-      const int chunk = (4 * h + i) ^ (r & 7);
+      const int cur = i & 1;
+      if (i < 3) {
+        read_a(i + 1, a[cur ^ 1]);
+        bq[cur ^ 1][0] = dequant8<BITS>(wc[0], i + 1, scur[0], bcur[0]);
+        bq[cur ^ 1][1] = dequant8<BITS>(wc[1], i + 1, scur[1], bcur[1]);
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xb[(mb * 32 + r) * 32 + chunk * 4]);
-        acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b0), acc[mb][0], 0, 0, 0);
-        acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b1), acc[mb][1], 0, 0, 0);
+        acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[cur][mb]), as_bf16x8(bq[cur][0]), acc[mb][0], 0, 0, 0);
+        acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[cur][mb]), as_bf16x8(bq[cur][1]), acc[mb][1], 0, 0, 0);
       }
     }
-    if (more) {
-      stage_store(buf ^ 1, xr);
+    // Issue order for the region above: the first k-step's operands, then
+    // for each k-step one MFMA at a time with the next k-step's LDS reads
+    // and dequantization threaded between them, so the matrix pipe never
+    // waits on a whole batch of reads or VALU work.
+    __builtin_amdgcn_sched_group_barrier(0x100, MB, 0); // DS reads of k-step 0
+    __builtin_amdgcn_sched_group_barrier(0x002, 24, 0); // part of its dequant
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+    for (int i = 0; i < 3; ++i) {
 #pragma unroll
-        for (int v = 0; v < kWV; ++v) wc[j][v] = wn[j][v];
-        scur[j] = sn[j];
-        bcur[j] = bn[j];
+      for (int g = 0; g < MB; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); // VALU
       }
+#pragma unroll
+      for (int g = 0; g < MB; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 2 * MB; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_store(buf ^ 1, xr);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int v = 0; v < kWV; ++v) wc[j][v] = wn[j][v];
+      scur[j] = sn[j];
+      bcur[j] = bn[j];
     }
     __syncthreads();
   }
