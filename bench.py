@@ -46,6 +46,22 @@ def algorithmic_bytes(M, N, K, bits, x_bytes=2, y_bytes=2, s_bytes=4):
     return N * K * bits // 8 + 2 * N * (K // GS) * s_bytes + M * K * x_bytes + M * N * y_bytes
 
 
+TRAFFIC_FILE = REPO / "profiles" / "bench_config2_hbm_traffic.md"
+
+
+def measured_traffic(label):
+    """Calibrated HBM bytes per dispatch of layer `label` ("fc1"/"fc2") from
+    the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary, with the kernel
+    it was measured on; None when the summary is absent."""
+    if not TRAFFIC_FILE.exists():
+        return None, None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 4 and parts[0] == "traffic" and parts[1] == label:
+            return int(parts[3]), parts[2]
+    return None, None
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,6 +71,9 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline work")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed steps, run one f32->bf16 copy of 2^27 elements (512 MiB read, "
+                         "256 MiB written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -182,6 +201,13 @@ def main():
         step(args.warmup + i, evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if args.copy_probe:
+        src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
+        dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     total_ms = evs[0][0].elapsed_time(evs[-1][3])
     ms_step = total_ms / args.steps
     k_fc1 = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
@@ -197,10 +223,11 @@ def main():
 
     # Dominant kernel's roofline (MFMA-bound at M = 1536: AI far above the ridge).
     if k_fc1 >= k_fc2:
-        dom, dom_ms, dom_flops, dom_layer = "qmm fc1 4-bit 1536x3072->12288", k_fc1, flops_fc1, fc1
+        dom, dom_ms, dom_flops, dom_layer, label = "qmm fc1 4-bit 1536x3072->12288", k_fc1, flops_fc1, fc1, "fc1"
     else:
-        dom, dom_ms, dom_flops, dom_layer = "qmm fc2 8-bit 1536x12288->3072", k_fc2, flops_fc2, fc2
+        dom, dom_ms, dom_flops, dom_layer, label = "qmm fc2 8-bit 1536x12288->3072", k_fc2, flops_fc2, fc2, "fc2"
     achieved = dom_flops / (dom_ms / 1e3) / 1e12
+    traffic, traffic_kernel = measured_traffic(label)
     roofline = {
         "kernel": dom,
         "bound": "mfma",
@@ -208,7 +235,9 @@ def main():
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": (f"{TRAFFIC_FILE.relative_to(REPO)} ({traffic_kernel}, rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                           "copy-calibrated)") if traffic else None,
         "flops_per_launch": dom_flops,
         "algorithmic_bytes_per_launch": algorithmic_bytes(M_TOKENS, dom_layer.N, dom_layer.K, dom_layer.bits),
         "avg_launch_ms": round(dom_ms, 4),
