@@ -114,6 +114,78 @@ template <> struct Load8<SDQ_FLOAT32> {
   }
 };
 
+// Buffer resources: a 32-bit byte window over a global array, addressed as
+// (per-lane VGPR offset) + (uniform SGPR offset).  A pipelined loop then
+// advances one scalar per step instead of 64-bit addresses per lane.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, int(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 bload16(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+__device__ __forceinline__ uint32_t bload2(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// One scale or bias element through a buffer resource, widened to f32.
+template <int DT> struct BLoadScalar;
+template <> struct BLoadScalar<SDQ_FLOAT32> {
+  static __device__ __forceinline__ float get(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __uint_as_float(bload4(r, voff, soff));
+  }
+};
+template <> struct BLoadScalar<SDQ_BFLOAT16> {
+  static __device__ __forceinline__ float get(Rsrc r, uint32_t voff, uint32_t soff) {
+    return bf16_bits_to_f32(bload2(r, voff, soff));
+  }
+};
+template <> struct BLoadScalar<SDQ_FLOAT16> {
+  static __device__ __forceinline__ float get(Rsrc r, uint32_t voff, uint32_t soff) {
+    return f16_bits_to_f32(bload2(r, voff, soff));
+  }
+};
+
+// Eight consecutive activations at byte offset voff + soff as a bf16x8 MFMA
+// operand (f16 and f32 are converted, rounding to nearest even).
+template <int DT> struct BLoad8;
+template <> struct BLoad8<SDQ_BFLOAT16> {
+  static __device__ __forceinline__ u32x4 get(Rsrc r, uint32_t voff, uint32_t soff) {
+    return bload16(r, voff, soff);
+  }
+};
+template <> struct BLoad8<SDQ_FLOAT16> {
+  static __device__ __forceinline__ u32x4 get(Rsrc r, uint32_t voff, uint32_t soff) {
+    const u32x4 v = bload16(r, voff, soff);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t pair = v[i];
+      o[i] = pack_bf16x2(f16_bits_to_f32(pair & 0xffffu), f16_bits_to_f32(pair >> 16));
+    }
+    return o;
+  }
+};
+template <> struct BLoad8<SDQ_FLOAT32> {
+  static __device__ __forceinline__ u32x4 get(Rsrc r, uint32_t voff, uint32_t soff) {
+    const u32x4 a = bload16(r, voff, soff);
+    const u32x4 b = bload16(r, voff + 16, soff);
+    u32x4 o;
+    o[0] = pack_bf16x2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    o[1] = pack_bf16x2(__uint_as_float(a[2]), __uint_as_float(a[3]));
+    o[2] = pack_bf16x2(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    o[3] = pack_bf16x2(__uint_as_float(b[2]), __uint_as_float(b[3]));
+    return o;
+  }
+};
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
   return __builtin_bit_cast(bf16x8, v);
 }

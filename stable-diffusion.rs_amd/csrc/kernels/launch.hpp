@@ -43,11 +43,26 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          int bits, const QmvPlan &plan, const SplitWorkspace &ws,
          hipStream_t stream);
 
+// Tile and split-K plan of one qmm launch (a pure function of the shape and
+// the CU count).
+struct QmmPlan {
+  int bm = 256;             // rows per block tile (128 or 256); tiles are bm x 256
+  int tiles_n = 0;          // tiles along N
+  int tiles = 0;            // all tiles, M-tile major
+  int dp_tiles = 0;         // tiles [0, dp_tiles) are computed whole
+  int splits = 1;           // K ranges of each later tile
+  int steps_per_split = 0;  // 64-wide K steps per range
+  int blocks = 0;           // grid size
+  size_t partial_floats = 0; // workspace needed (0 without split tiles)
+  int counters = 0;         // split tiles
+};
+
 // y [M, N] = x [M, K] @ dequantize(w).T for any M.  qmm.hip.
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus);
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, hipStream_t stream);
+         int bits, const QmmPlan &plan, const SplitWorkspace &ws, hipStream_t stream);
 
 // Elementwise helpers (elementwise.hip).  n = element count.
 void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,

@@ -124,6 +124,26 @@ def test_split_k_is_deterministic_and_correct(oracle, sdq, stream, M):
         assert np.array_equal(q.matmul(x_dev, stream).to_numpy(), first)
 
 
+@pytest.mark.parametrize("M,N,K,bits", [
+    (300, 512, 8192, 4),    # 4 tiles of 256 x 256: every tile split along K
+    (100, 640, 4096, 8),    # 128-row tiles, 3 tiles, split
+    (4352, 4096, 512, 4),   # 272 tiles: one whole round, the last 16 tiles split
+])
+def test_large_m_split_k_is_deterministic_and_correct(oracle, sdq, stream, M, N, K, bits):
+    # When the tiles do not fill whole rounds of CUs, the MFMA kernel splits
+    # the tiles of the last round along K; the last block of each such tile
+    # adds the partials in range order, so repeated calls agree bit for bit.
+    print(f"qmm split-K M={M} N={N} K={K} bits={bits}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 930 + M + bits, N, K, bits)
+    x_dev, x_vals = _x(oracle, sdq, 931 + M, (M, K), "bf16")
+    first = q.matmul(x_dev, stream).to_numpy()
+    last = np.arange(max(0, M - 256), M)  # the split tiles are the last M tile
+    pick = np.unique(np.concatenate([last, np.linspace(0, M - 1, 32).astype(int)]))
+    _check(first[pick], x_vals[pick], deq)
+    for _ in range(2):
+        assert np.array_equal(q.matmul(x_dev, stream).to_numpy(), first)
+
+
 def test_repeated_calls_are_identical(oracle, sdq, stream):
     q, _ = _qweight(oracle, sdq, stream, 950, 512, 1024, 8)
     x_dev, _ = _x(oracle, sdq, 951, (300, 1024), "bf16")
