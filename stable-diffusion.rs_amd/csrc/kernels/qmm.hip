@@ -77,7 +77,7 @@ struct QmmWork {
   unsigned *counters;
 };
 
-template <int BITS, int XDT, int SDT, int ODT, int BM, int GS>
+template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH>
 __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
@@ -176,6 +176,32 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     dst[1] = dequant8<BITS>(ws.q[1], i, ws.s[1], ws.b[1]);
   };
 
+  // Scale and bias chunks (SCH): a 16-byte load brings kCG consecutive
+  // groups of one row, so each row's scales and biases cost one load per
+  // kCG groups instead of one per step -- a load instruction's cost is set
+  // by the distinct cache lines it touches (32 rows here), not its bytes.
+  // Needs 16-byte aligned scale rows; the host picks SCH accordingly.
+  constexpr int kCG = 16 / int(sizeof(ST));
+  auto chunk_of = [&](int step) { return ((step * 64) / GS) / kCG; };
+  auto load_chunk = [&](int c, u32x4 (&cs)[2], u32x4 (&cb)[2]) {
+    const uint32_t off = uint32_t(c) * 16;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      cs[j] = bload16(rs, soff[j], off);
+      cb[j] = bload16(rb, soff[j], off);
+    }
+  };
+  auto pick = [&](const u32x4 &v, int e) -> float {
+    if constexpr (sizeof(ST) == 4) {
+      const uint32_t wv = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
+      return __uint_as_float(wv);
+    } else {
+      const int d = e >> 1;
+      const uint32_t wv = d == 0 ? v[0] : d == 1 ? v[1] : d == 2 ? v[2] : v[3];
+      return Elem<SDT>::load(typename Elem<SDT>::T((e & 1) ? (wv >> 16) : (wv & 0xffffu)));
+    }
+  };
+
   floatx16 acc[MB][2];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -188,9 +214,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   //   * weights: codes, scales and biases of step s + 2 are loaded at the top
   //     of step s (a three-deep register queue);
   //   * activations: the tile of step s + 2 arrives in registers during step
-  //     s - 1 and is written to LDS stage (s + 2) % 3 halfway through step s,
-  //     when the tile of step s + 3 is requested; one barrier per step makes
-  //     it visible;
+  //     s - 1 and is written to LDS stage (s + 2) % 3 in the third k-step of
+  //     step s, when the tile of step s + 3 is requested; one barrier per
+  //     step makes it visible;
   //   * operands: the A fragments and dequantized B fragments of k-step i + 1
   //     are prepared while the MFMAs of k-step i run -- across the step
   //     boundary too, since stage (s + 1) % 3 is complete before step s ends.
@@ -205,6 +231,17 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   stage_load(min(k_begin + 2, k_last), xr);
   load_w(k_begin, w0);
   load_w(min(k_begin + 1, k_last), w1);
+  // SCH: one chunk in registers, always the one holding step s + 1 at the
+  // top of step s.  That step's scale and bias are picked from it there (the
+  // weight queue entry of step s + 1 was loaded without them), then the chunk
+  // of step s + 2 is loaded if it differs -- a full step before its first
+  // pick, and with no register copy that would wait for the load.
+  u32x4 cs[2], cb[2];
+  int c_cur = 0;
+  if constexpr (SCH) {
+    c_cur = chunk_of(min(k_begin + 1, k_last));
+    load_chunk(c_cur, cs, cb);
+  }
   __syncthreads();
 
   u32x4 a[MB];
@@ -213,52 +250,186 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   for (int mb = 0; mb < MB; ++mb) a[mb] = read_a(xs, 0, mb);
   dequant(w0, 0, bq[0]);
 
+  // Dequantization of one k-step for both 32-row blocks of weights, cut into
+  // pieces that are spread over the MFMA slots below (block j's pieces are
+  // numbered j * kPieces + piece).  4-bit: piece 0 splits the word into even
+  // and odd codes, pieces 1-4 each produce one packed bf16 pair.  8-bit:
+  // pieces 0-3 each produce one pair.
+  constexpr int kPieces = BITS == 4 ? 5 : 4;
+  constexpr int kSlots = 2 * MB;    // MFMAs per k-step
+  constexpr int kRefillLag = 4;     // slots between an A fragment's last MFMA and its refill
+  uint32_t lo[2], hi[2];
+  auto dq_piece = [&](const WStep &ws, int i, int j, int piece, u32x4 &dst) {
+    const float sc_ = ws.s[j], bi_ = ws.b[j];
+    if constexpr (BITS == 4) {
+      if (piece == 0) {
+        const uint32_t wd = ws.q[j][0][i];
+        lo[j] = opaque(wd & 0x0F0F0F0Fu);        // codes 0, 2, 4, 6
+        hi[j] = opaque((wd >> 4) & 0x0F0F0F0Fu); // codes 1, 3, 5, 7
+      } else {
+        const int d = piece - 1;
+        dst[d] = pack_bf16x2(fmaf(byte_f(lo[j], d), sc_, bi_), fmaf(byte_f(hi[j], d), sc_, bi_));
+      }
+    } else {
+      const uint32_t wd = ws.q[j][i / 2][(i % 2) * 2 + piece / 2];
+      const int e = 2 * (piece % 2);
+      dst[piece] = pack_bf16x2(fmaf(byte_f(wd, e), sc_, bi_), fmaf(byte_f(wd, e + 1), sc_, bi_));
+    }
+  };
+
   int st0 = 0; // LDS stage of step s; s + 1 and s + 2 follow cyclically
   for (int step = k_begin; step < k_end; ++step) {
     const int st1 = st0 == 2 ? 0 : st0 + 1;
     const int st2 = st1 == 2 ? 0 : st1 + 1;
-    load_w(min(step + 2, k_last), w2);
+    const int wstep = min(step + 2, k_last);
+    const int xstep = min(step + 3, k_last);
+    if constexpr (SCH) {
+      const int e1 = (min(step + 1, k_last) * 64) / GS - c_cur * kCG;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        w1.s[j] = pick(cs[j], e1);
+        w1.b[j] = pick(cb[j], e1);
+      }
+      const int c2 = chunk_of(wstep);
+      if (c2 != c_cur) {
+        c_cur = c2;
+        load_chunk(c2, cs, cb);
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
+    // Issue order is fixed by hand: every MFMA is followed by one small
+    // piece of other work -- a slice of the next k-step's dequantization, an
+    // LDS read refilling an A fragment, in k-step 0 the weight loads and in
+    // k-step 2 the staging store and the next activation load -- so that the
+    // matrix pipe and the VALU work side by side, global loads are spread
+    // over the step, and no wait blocks a whole batch.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = i & 1;
-      if (i == 1) {
-        stage_store(xs + st2 * kStage, xr);
-        stage_load(min(step + 3, k_last), xr);
-      }
-      if (i < 3)
-        dequant(w0, i + 1, bq[c ^ 1]);
-      else
-        dequant(w1, 0, bq[c ^ 1]);
-      // Each A fragment is refilled for the next k-step (the next step's
-      // first k-step after the last) as soon as its two MFMAs are issued.
-      const uint32_t *nsrc = xs + (i < 3 ? st0 : st1) * kStage;
-      const int ni = i < 3 ? i + 1 : 0;
+      const WStep &wsrc = i < 3 ? w0 : w1;
+      const int di = i < 3 ? i + 1 : 0;
+      const uint32_t *csrc = xs + st0 * kStage;                 // this k-step's stage
+      const uint32_t *nsrc = xs + (i < 3 ? st0 : st1) * kStage; // the next k-step's
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[mb]), as_bf16x8(bq[c][0]), acc[mb][0], 0, 0, 0);
-        acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[mb]), as_bf16x8(bq[c][1]), acc[mb][1], 0, 0, 0);
-        a[mb] = read_a(nsrc, ni, mb);
-      }
-      // One MFMA at a time, with the next k-step's LDS reads, dequant VALU
-      // and (halfway) the staging traffic threaded between them.
+      for (int t = 0; t < kSlots; ++t) {
+        const int mb = t >> 1, j = t & 1;
+        acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[mb]), as_bf16x8(bq[c][j]), acc[mb][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Dequantization pieces of the next k-step, spread evenly.
 #pragma unroll
-      for (int g = 0; g < MB; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
-        if (i == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); // DS write
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); // VALU
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-        if (i == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); // VALU
+        for (int pc = 0; pc < 2 * kPieces; ++pc)
+          if ((pc * kSlots) / (2 * kPieces) == t)
+            dq_piece(wsrc, di, pc / kPieces, pc % kPieces, bq[c ^ 1][pc / kPieces]);
+        // A fragment m is refilled kRefillLag slots after its second MFMA,
+        // once that MFMA has surely read it; the last fragments of a k-step
+        // are refilled early in the next one, before their own use.
+        if (j == 1) {
+          const int m = (((t - kRefillLag - 1) % kSlots + kSlots) % kSlots) >> 1;
+          if (t >= kRefillLag + 1)
+            a[m] = read_a(nsrc, i < 3 ? i + 1 : 0, m); // used in the next k-step
+          else
+            a[m] = read_a(csrc, i, m);                 // used later in this one
+        }
+        if (i == 2) {
+          const int q = mb;
+          if (j == 0) {
+            const int row = sr + 32 * q;
+            *reinterpret_cast<u32x4 *>(&xs[st2 * kStage + row * 32 + ((sc ^ ((row >> 1) & 7)) * 4)]) = xr[q];
+          } else {
+            xr[q] = BLoad8<XDT>::get(rx, xoff[q], uint32_t(xstep) * 64 * sizeof(XT));
+          }
+        }
+        if (i == 0 && t >= kSlots - 2) {
+          // This step's share of the weight queue: step s + 2, one 32-row
+          // block per slot.
+          const int jj = t - (kSlots - 2);
+          const uint32_t wso = uint32_t(wstep) * kWordsPerStep * 4;
+          const uint32_t sso = uint32_t((wstep * 64) / GS) * sizeof(ST);
+#pragma unroll
+          for (int v = 0; v < kWV; ++v) w2.q[jj][v] = bload16(rw, woff[jj] + 16 * v, wso);
+          if constexpr (!SCH) {
+            w2.s[jj] = BLoadScalar<SDT>::get(rs, soff[jj], sso);
+            w2.b[jj] = BLoadScalar<SDT>::get(rb, soff[jj], sso);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     w0 = w1;
     w1 = w2;
     st0 = st1;
     __syncthreads();
   }
+
+  // Output.  Accumulator entry e of lane (r, h) in tile (mb, j) is row
+  // 32*mb + 8*(e/4) + 4*h + e%4, column 32*j + r of the wave's slab: one
+  // store per element would write 2-byte pieces of two rows per instruction,
+  // and the cost of a store is per instruction.  So each wave stages its
+  // slab through its own part of the (now idle) LDS, a few 32-row blocks at
+  // a time, and writes whole 128-byte row pieces with 16-byte stores (single
+  // elements where the output rows are not 16-byte aligned).
+  using OT = typename Elem<ODT>::T;
+  constexpr int kChunkElems = 16 / int(sizeof(OT));
+  constexpr int kCpr = 64 / kChunkElems;                 // 16-byte chunks per slab row
+  constexpr int kRowBytes = 64 * int(sizeof(OT)) + 16;   // padded: no bank conflicts
+  constexpr int kWaveLds = 3 * kStage * 4 / 4;           // LDS bytes per wave
+  constexpr int kPassMB = (kWaveLds / kRowBytes) / 32 >= 4 && MB % 4 == 0 ? 4
+                          : (kWaveLds / kRowBytes) / 32 >= 2 && MB % 2 == 0 ? 2 : 1;
+  static_assert(kPassMB * 32 * kRowBytes <= kWaveLds, "output staging exceeds the LDS");
+  auto store_tile = [&](auto produce) {
+    const bool vec = N % kChunkElems == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    uint8_t *wl = reinterpret_cast<uint8_t *>(xs) + wave * kWaveLds;
+#pragma unroll
+    for (int p0 = 0; p0 < MB; p0 += kPassMB) {
+#pragma unroll
+      for (int mb = p0; mb < p0 + kPassMB; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float v[16];
+          produce(mb, j, v);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int row = 32 * (mb - p0) + 8 * (e / 4) + 4 * h + (e % 4);
+            *reinterpret_cast<OT *>(wl + row * kRowBytes + (32 * j + r) * int(sizeof(OT))) =
+                Elem<ODT>::store(v[e]);
+          }
+        }
+      }
+      // The slab is read back by other lanes of this wave only.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int it = 0; it < kPassMB * 32 * kCpr / 64; ++it) {
+        const int idx = it * 64 + lane;
+        const int row = idx / kCpr, chunk = idx % kCpr;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(wl + row * kRowBytes + chunk * 16);
+        const int grow = m0 + 32 * p0 + row;
+        const int gcol = nw + chunk * kChunkElems;
+        if (grow < M) {
+          OT *dst = y + int64_t(grow) * N + gcol;
+          if (vec) {
+            if (gcol < N) *reinterpret_cast<u32x4 *>(dst) = v;
+          } else {
+            // Rows not 16-byte aligned, or a ragged last chunk: element stores.
+#pragma unroll
+            for (int q = 0; q < kChunkElems; ++q) {
+              if (gcol + q < N) {
+                const uint32_t word = v[(q * int(sizeof(OT))) / 4];
+                if constexpr (sizeof(OT) == 4)
+                  dst[q] = __builtin_bit_cast(OT, word);
+                else
+                  dst[q] = OT((q & 1) ? (word >> 16) : (word & 0xffffu));
+              }
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  };
 
   if (bid >= wk.dp_tiles) {
     // A K range of a split tile.  Its accumulators go out as agent-scope
@@ -290,47 +461,30 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     }
     __syncthreads();
     if (!s_last) return;
+    // The sums go straight to the output: writing them back into the
+    // accumulators would make the register allocator copy accumulators
+    // inside the main loop.
+    store_tile([&](int mb, int j, float (&sum)[16]) {
+      for (int p = 0; p < wk.splits; ++p) {
+        const float *src = base + int64_t(p) * (kRegs * kThreads) + ((mb * 2 + j) * 16) * kThreads;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const floatx16 own = acc[mb][j];
-        floatx16 sum;
-        for (int p = 0; p < wk.splits; ++p) {
-          floatx16 t;
-          if (p == split) {
-            t = own;
-          } else {
-            const float *src = base + int64_t(p) * (kRegs * kThreads);
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-              t[e] = __hip_atomic_load(src + ((mb * 2 + j) * 16 + e) * kThreads, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-          }
-          sum = p == 0 ? t : sum + t;
+        for (int e = 0; e < 16; ++e) {
+          const float t = p == split ? acc[mb][j][e]
+                                     : __hip_atomic_load(src + e * kThreads, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+          sum[e] = p == 0 ? t : sum[e] + t;
         }
-        acc[mb][j] = sum;
       }
-    }
+    });
     if (tid == 0)
       __hip_atomic_store(&wk.counters[sk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
 
-  // Accumulator entry e of lane (r, h) in tile (mb, j) is row
-  // 32*mb + 8*(e/4) + 4*h + e%4, column 32*j + r of the wave's slab.
+  store_tile([&](int mb, int j, float (&v)[16]) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = nw + 32 * j + r;
-      if (col >= N) continue;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + 32 * mb + 8 * (e / 4) + 4 * h + (e % 4);
-        if (row < M) y[int64_t(row) * N + col] = Elem<ODT>::store(acc[mb][j][e]);
-      }
-    }
-  }
+    for (int e = 0; e < 16; ++e) v[e] = acc[mb][j][e];
+  });
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int BM>
@@ -344,10 +498,20 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
   auto *xp = static_cast<const typename Elem<XDT>::T *>(x);
   auto *sp = static_cast<const typename Elem<SDT>::T *>(s);
   auto *bp = static_cast<const typename Elem<SDT>::T *>(b);
-  if (gs == 64)
-    qmm_kernel<BITS, XDT, SDT, ODT, BM, 64><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk);
-  else
-    qmm_kernel<BITS, XDT, SDT, ODT, BM, 128><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk);
+  // Chunked scale loads need every scale row 16-byte aligned.
+  const size_t srow_bytes = size_t(K / gs) * sizeof(typename Elem<SDT>::T);
+  const bool sch = srow_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(s) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(b) % 16 == 0;
+#define SDQ_QMM_LAUNCH(G, C) \
+  qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk)
+  if (gs == 64) {
+    if (sch) SDQ_QMM_LAUNCH(64, true);
+    else SDQ_QMM_LAUNCH(64, false);
+  } else {
+    if (sch) SDQ_QMM_LAUNCH(128, true);
+    else SDQ_QMM_LAUNCH(128, false);
+  }
+#undef SDQ_QMM_LAUNCH
 }
 
 template <int BITS, int XDT, int SDT, int ODT>

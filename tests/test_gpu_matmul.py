@@ -144,6 +144,21 @@ def test_large_m_split_k_is_deterministic_and_correct(oracle, sdq, stream, M, N,
         assert np.array_equal(q.matmul(x_dev, stream).to_numpy(), first)
 
 
+@pytest.mark.parametrize("sdt", ["f32", "bf16"])
+@pytest.mark.parametrize("M,N", [(70, 97), (300, 250), (33, 6)])
+def test_ragged_output_rows(oracle, sdq, stream, sdt, M, N):
+    # Output rows that are not a whole number of 16-byte pieces (f32 or bf16
+    # output) take the element-store path of the MFMA kernel's epilogue.
+    print(f"ragged N M={M} N={N} scales={sdt}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 970 + N, N, 192, 4, sdt=sdt)
+    x_dev, x_vals = _x(oracle, sdq, 971 + M, (M, 192), "bf16")
+    y = q.matmul(x_dev, stream)
+    got = y.to_numpy()
+    if y.dtype == sdq.BFLOAT16:
+        got = sdq.bf16_bits_to_f32(got).reshape(M, N)
+    _check(got, x_vals, deq)
+
+
 def test_repeated_calls_are_identical(oracle, sdq, stream):
     q, _ = _qweight(oracle, sdq, stream, 950, 512, 1024, 8)
     x_dev, _ = _x(oracle, sdq, 951, (300, 1024), "bf16")
