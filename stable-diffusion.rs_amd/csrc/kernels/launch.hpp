@@ -21,22 +21,24 @@ void dequantize(const uint32_t *wq, const void *scales, const void *biases,
                 int s_dtype, int64_t rows, int64_t cols, int group_size,
                 int bits, void *out, int out_dtype, hipStream_t stream);
 
-// Workspace the small-M kernel uses when it splits K across blocks.  The
-// counters must be zero on entry; the kernel leaves them zero.
+// Workspace the matmul kernels use when they split K across blocks: partial
+// tiles and one counter per split tile.  The counters must be zero on entry;
+// the kernels leave them zero.
 struct SplitWorkspace {
-  float *partial = nullptr;     // [splits, M, N] floats
-  unsigned *counters = nullptr; // [ceil(N/32)]
+  float *partial = nullptr;
+  unsigned *counters = nullptr;
 };
 
 struct QmvPlan {
-  int splits = 1;
-  int groups_per_split = 0;
+  int waves = 4;             // waves (32-row tiles) per block: 1 or 4
+  int splits = 1;            // K ranges
+  int groups_per_split = 0;  // 64-wide steps per range
   size_t partial_floats = 0; // workspace needed (0 when splits == 1)
-  int counters = 0;
+  int counters = 0;          // 32-row tiles
 };
 
 // y [M, N] = x [M, K] @ dequantize(w).T for M <= 32.  qmv.hip.
-QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int cus);
+QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus);
 void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,

@@ -4,36 +4,35 @@
 // modulation linears at M = 1, sd-models/src/mlx/flux.rs:279-299, 437, and the
 // T5 FFN at few tokens, t5.rs:209-214).
 //
-// Time here is the packed weight stream, so the kernel keeps VALU work per
-// weight element small and many weight bytes in flight:
+// Time here is the packed weight stream, so everything is arranged to keep
+// many whole cache lines of codes in flight and little other work per byte:
 //
+//   * A block is four waves; wave v owns one 32-row tile of weights (the MFMA
+//     N side) over the block's range of K.  K is split so that the grid is
+//     about two blocks per CU, all resident at once.
+//   * Codes stream in row chunks of 128 bytes (four 64-wide steps at 4 bits,
+//     two at 8): each load instruction brings eight whole rows' chunks, i.e.
+//     eight full cache lines (a load's cost is set by the cache lines it
+//     touches), with kDepth chunks in flight per wave.  A small wave-private
+//     LDS buffer turns them around into the MFMA operand layout.
 //   * Codes are never dequantized element by element.  For one 64-wide step
-//     of K (one group at group size 64; half a group at 128) the MFMA
-//     computes t[m][n] = sum_k x[m,k] * c_k with c_k = q_k + OFF held EXACTLY
-//     in bf16 (4-bit: OFF = 128 and the bf16 pattern 0x4300|q is built with
-//     one byte-permute and one and-or per pair; 8-bit: OFF = 0, q converted).
-//     Then y += s * t + (b - OFF*s) * X, where X[m] = sum_k x[m,k] over the
-//     step.  The affine dequantization is applied once per group per output
-//     instead of once per weight, and is more accurate than rounding each
-//     dequantized weight to bf16.
-//   * A block of eight waves owns 32 weight rows (the MFMA's N side) and a
-//     range of K.  It first stages its rows of x (bf16) and their per-step
-//     sums in LDS, so that the only global traffic of the main loop is the
-//     weight stream: each wave keeps a queue of kDepth steps of packed codes,
-//     scales and biases in registers, loaded unconditionally so every wait
-//     covers exactly one queue slot.
-//   * When there are too few 32-row tiles to fill the chip, K is split across
-//     blocks.  Partial sums are written with agent-scope (L2-bypassing)
-//     stores; after they complete, the block bumps the tile's counter; the
-//     last block reads the partials back with agent-scope loads and adds them
-//     in split order, so the result is deterministic and no cache-wide
-//     writeback or invalidate is needed.
+//     of K the MFMA computes t[m][n] = sum_k x[m,k] * c_k with c_k = q_k + OFF
+//     held EXACTLY in bf16 (4-bit: OFF = 128, the bf16 pattern 0x4300|q built
+//     by byte permutes; 8-bit: OFF = 0, q converted).  Then
+//     y += s * t + (b - OFF*s) * X, where X[m] = sum_k x[m,k] over the step:
+//     the affine dequantization is applied once per group per output, and is
+//     more accurate than rounding each dequantized weight to bf16.
+//   * x[0:M, range] (bf16, zero past the range), its per-step sums and the
+//     tiles' scales and biases for the range are staged in LDS once per
+//     block with coalesced loads, so the loop's only global traffic is codes.
+//   * When K is split across blocks, each wave writes its partial tile with
+//     agent-scope (L2-bypassing) stores and counts itself in; the last wave
+//     to arrive for a tile adds the partials in split order (deterministic)
+//     and re-arms the counter.
 //   * MFMA v_mfma_f32_32x32x16_bf16 with the tokens on the M side.  Lane
 //     (r, h) = (lane % 32, lane / 32) feeds token r and weight row r; its
-//     eight K elements of k-step i are k = 64*step + 32*h + 8*i + e, so each
-//     lane's weight bytes for a step are one contiguous 16 B (4-bit) or 32 B
-//     (8-bit) load.  Token rows r >= M read row M - 1; their results are
-//     never stored.
+//     eight K elements of k-step i are k = 64*step + 32*h + 8*i + e.  Token
+//     rows r >= M read row M - 1; their results are never stored.
 #include <algorithm>
 
 #include "device_common.hpp"
@@ -46,127 +45,218 @@ namespace {
 
 using namespace dev;
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kDepth = 8;            // weight steps in flight per wave
-constexpr int kXBudget = 48 * 1024;  // LDS bytes for the staged rows of x
+constexpr int kWRow = 144;         // LDS bytes per staged weight row (128 + pad)
+constexpr int kWBuf = 32 * kWRow;  // one wave's chunk buffer
+constexpr int kLdsBudget = 64 * 1024;
 
-// Eight 4-bit codes of `wd`, in element order, as bf16 (128 + q): exact.
+__host__ __device__ constexpr int chunk_steps(int bits) { return bits == 4 ? 4 : 2; }
+
+// Eight 4-bit codes of `wd` as bf16 (128 + q), exact, in the order
+// q0 q2 q4 q6 q1 q3 q5 q7: each pair is one byte permute of the even or odd
+// codes with the constant exponent byte 0x43 (bf16 0x43nn = 128 + nn for
+// nn < 128).  The staged x uses the same order within each eight elements.
 __device__ __forceinline__ u32x4 codes4_plus128(uint32_t wd) {
-  const uint32_t s4 = wd >> 4;
+  const uint32_t lo = wd & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
+  const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
+  const uint32_t c43 = 0x43434343u;
   u32x4 r;
-  // byte 0 <- wd.byte[d] (low nibble q[2d]), byte 2 <- s4.byte[d] (low
-  // nibble q[2d+1]), bytes 1 and 3 <- 0; then keep the nibbles and set the
-  // bf16 exponent of 128.
-  r[0] = (__builtin_amdgcn_perm(s4, wd, 0x0C040C00u) & 0x000F000Fu) | 0x43004300u;
-  r[1] = (__builtin_amdgcn_perm(s4, wd, 0x0C050C01u) & 0x000F000Fu) | 0x43004300u;
-  r[2] = (__builtin_amdgcn_perm(s4, wd, 0x0C060C02u) & 0x000F000Fu) | 0x43004300u;
-  r[3] = (__builtin_amdgcn_perm(s4, wd, 0x0C070C03u) & 0x000F000Fu) | 0x43004300u;
+  r[0] = __builtin_amdgcn_perm(c43, lo, 0x04010400u); // (q0, q2)
+  r[1] = __builtin_amdgcn_perm(c43, lo, 0x04030402u); // (q4, q6)
+  r[2] = __builtin_amdgcn_perm(c43, hi, 0x04010400u); // (q1, q3)
+  r[3] = __builtin_amdgcn_perm(c43, hi, 0x04030402u); // (q5, q7)
   return r;
+}
+
+// Eight bf16 values e0..e7 reordered to e0 e2 e4 e6 e1 e3 e5 e7.
+__device__ __forceinline__ u32x4 even_odd(const u32x4 &v) {
+  const uint32_t v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+  u32x4 o;
+  o[0] = __builtin_amdgcn_perm(v1, v0, 0x05040100u); // (e0, e2)
+  o[1] = __builtin_amdgcn_perm(v3, v2, 0x05040100u); // (e4, e6)
+  o[2] = __builtin_amdgcn_perm(v1, v0, 0x07060302u); // (e1, e3)
+  o[3] = __builtin_amdgcn_perm(v3, v2, 0x07060302u); // (e5, e7)
+  return o;
 }
 
 // Eight 8-bit codes (two words), in element order, as bf16 q: exact.
 __device__ __forceinline__ u32x4 codes8(uint32_t w0, uint32_t w1) {
+  const uint32_t a = opaque(w0), b = opaque(w1);
   u32x4 r;
-  r[0] = pack_bf16x2(float(w0 & 0xffu), float((w0 >> 8) & 0xffu));
-  r[1] = pack_bf16x2(float((w0 >> 16) & 0xffu), float(w0 >> 24));
-  r[2] = pack_bf16x2(float(w1 & 0xffu), float((w1 >> 8) & 0xffu));
-  r[3] = pack_bf16x2(float((w1 >> 16) & 0xffu), float(w1 >> 24));
+  r[0] = pack_bf16x2(float(a & 0xffu), float((a >> 8) & 0xffu));
+  r[1] = pack_bf16x2(float((a >> 16) & 0xffu), float(a >> 24));
+  r[2] = pack_bf16x2(float(b & 0xffu), float((b >> 8) & 0xffu));
+  r[3] = pack_bf16x2(float((b >> 16) & 0xffu), float(b >> 24));
   return r;
 }
-
-template <int BITS> struct Stage {
-  u32x4 w[BITS / 4]; // this lane's half-row of the step: 16 B or 32 B
-  float s, b;
-};
 
 // Row stride, in bf16 elements, of the staged x: 16 bytes of padding keep
 // consecutive rows on different LDS banks.
 __host__ __device__ constexpr int x_stride(int steps) { return steps * 64 + 8; }
 
-template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS>
-__global__ __launch_bounds__(kThreads) void qmv_kernel(
+// LDS layout of one block of `waves` waves (bytes): staged x, per-step
+// sums, scales and biases, the waves' chunk buffers.
+struct QmvLds {
+  int x, xsum, sb, wbuf, total;
+};
+
+__host__ __device__ inline QmvLds qmv_lds(int waves, int M, int mrows, int steps_pad,
+                                          int groups_range) {
+  QmvLds l;
+  l.x = 0;
+  l.xsum = (M * x_stride(steps_pad) * 2 + 15) & ~15;
+  l.sb = l.xsum + steps_pad * mrows * 4;
+  l.wbuf = (l.sb + waves * 32 * groups_range * 8 + 15) & ~15;
+  l.total = l.wbuf + waves * kWBuf;
+  return l;
+}
+
+// WAVES waves per block (4 when K is split into short ranges, 1 when each
+// wave streams a long range), DEPTH code chunks in flight per wave.
+template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS, int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
     const typename Elem<SDT>::T *__restrict__ scales,
     const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K,
-    int steps_per_split, float *__restrict__ partial, unsigned *__restrict__ counters) {
-  using XT = typename Elem<XDT>::T;
-  using ST = typename Elem<SDT>::T;
+    int steps_per_split, int groups_range, float *__restrict__ partial,
+    unsigned *__restrict__ counters) {
+  constexpr int kWaves = WAVES;
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int kDepth = DEPTH;
   constexpr float kOff = BITS == 4 ? 128.0f : 0.0f;
-  constexpr int kWordsPerStep = 64 * BITS / 32; // 8 or 16
-  constexpr int kHalfWords = kWordsPerStep / 2;
-  constexpr int kAcc = MROWS / 2; // accumulator entries holding rows < MROWS
+  constexpr int kC = chunk_steps(BITS);      // steps per 128-byte row chunk
+  constexpr int kStepBytes = 64 * BITS / 8;  // one row's codes per step
+  constexpr int kAcc = MROWS / 2;            // accumulator entries holding rows < MROWS
 
   const int steps = K / 64;
   const int groups = K / GS;
-  const int tile = blockIdx.x;
+  const int tiles = (N + 31) / 32;
   const int split = blockIdx.y;
   const int nsplit = gridDim.y;
-  const int s_begin = split * steps_per_split;
-  const int s_end = min(steps, s_begin + steps_per_split);
-  const int ns = s_end - s_begin; // >= 1 by construction of the plan
+  const int s0 = split * steps_per_split;
+  const int s1 = min(steps, s0 + steps_per_split);
+  const int ns = s1 - s0;                               // >= 1 by the plan
+  const int nchunks = (ns + kC - 1) / kC;
+  const int spad = (steps_per_split + kC - 1) / kC * kC; // staged steps, as laid out
+  const int g0 = (s0 * 64) / GS;
+  const int gr = groups_range;                          // groups staged per row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r = lane & 31;
   const int h = lane >> 5;
+  const int tile = blockIdx.x * kWaves + wave;
+  const bool live = tile < tiles;
+  const int tl = live ? tile : tiles - 1; // idle waves shadow the last tile, store nothing
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int xs_stride = x_stride(ns);
-  uint16_t *xl = reinterpret_cast<uint16_t *>(smem);                         // [M][xs_stride] bf16
-  float *xsum = reinterpret_cast<float *>(smem + size_t(M) * xs_stride * 2);  // [ns][MROWS]
-  float *red = reinterpret_cast<float *>(smem);                               // [kWaves][MROWS][32], after the loop
+  const QmvLds L = qmv_lds(kWaves, M, MROWS, spad, gr);
+  const int xs_stride = x_stride(spad);
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem + L.x);     // [M][xs_stride] bf16
+  float *xsum = reinterpret_cast<float *>(smem + L.xsum);     // [spad][MROWS]
+  float *sbl = reinterpret_cast<float *>(smem + L.sb);        // [waves][32][gr][2]
+  unsigned char *wbuf = smem + L.wbuf + wave * kWBuf;         // this wave's chunk buffer
 
-  // 1. This wave's weight queue goes out first, so its latency overlaps the
-  //    staging of x below.  The wave's steps are local steps wave,
-  //    wave + kWaves, ...
-  const int n = tile * 32 + r;
-  const int nrow = n < N ? n : N - 1; // rows past N are read, never stored
-  const uint32_t *wrow = w + int64_t(nrow) * (int64_t(K) * BITS / 32) + h * kHalfWords;
-  const ST *srow = scales + int64_t(nrow) * groups;
-  const ST *brow = biases + int64_t(nrow) * groups;
-  const uint16_t *arow = xl + (r < M ? r : M - 1) * xs_stride + 32 * h;
-
-  auto load_stage = [&](int sl, Stage<BITS> &st) {
-    const int step = s_begin + sl;
-    const uint32_t *wp = wrow + int64_t(step) * kWordsPerStep;
+  // Code chunks: lane L of load i brings bytes 16*(L%8) .. +16 of row
+  // 8*i + L/8's chunk, eight whole lines per load.  Chunks past the range
+  // are addressed beyond the buffer's end: such loads return zeros without
+  // touching memory, and their slots are never computed.
+  const Rsrc rw = make_rsrc(w, uint32_t(int64_t(N) * K * BITS / 8));
+  uint32_t woff[4];
 #pragma unroll
-    for (int v = 0; v < BITS / 4; ++v) st.w[v] = *reinterpret_cast<const u32x4 *>(wp + 4 * v);
-    const int gi = (step * 64) / GS;
-    st.s = Elem<SDT>::load(srow[gi]);
-    st.b = Elem<SDT>::load(brow[gi]);
-  };
-
-  // A queue of kDepth steps in registers: slot d holds this wave's step
-  // base + d; after computing it, the slot is refilled with step
-  // base + d + kDepth.  Slots past the last step hold a valid (wasted) step
-  // computed with zero weight, so the body is straight-line and the queue
-  // stays in issue order.
-  const int my_steps = ns > wave ? (ns - wave + kWaves - 1) / kWaves : 0;
-  auto local_step = [&](int i) {
-    const int sl = wave + kWaves * i;
-    return sl < ns ? sl : ns - 1;
-  };
-  Stage<BITS> q[kDepth];
+  for (int i = 0; i < 4; ++i) {
+    const int n = tl * 32 + 8 * i + (lane >> 3);
+    woff[i] = uint32_t(int64_t(n < N ? n : N - 1) * (int64_t(K) * BITS / 8) + 16 * (lane & 7));
+  }
+  auto load_chunk = [&](int c, u32x4 (&dst)[4]) {
+    const uint32_t so = c < nchunks ? uint32_t(s0 + c * kC) * kStepBytes : 0x80000000u;
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) load_stage(local_step(d), q[d]);
-  // 2. Stage x[0:M, K range] as bf16, 16-byte chunks.
-  {
-    const int chunks_per_row = ns * 8;
-    for (int c = tid; c < M * chunks_per_row; c += kThreads) {
+    for (int i = 0; i < 4; ++i) dst[i] = bload16(rw, woff[i], so);
+  };
+  u32x4 q[kDepth][4];
+
+  // 1. Stage x[0:M, s0*64 : (s0+spad)*64] as bf16, zero past the range (at
+  //    4 bits each eight elements in the codes' even/odd order), and the
+  //    waves' scales and biases, kBatch loads per thread at a time.  The
+  //    first batch's loads go out before the wave's first kDepth code chunks
+  //    and are stored after them: the wait for the staging then does not
+  //    include the chunks (loads complete in issue order for the counter),
+  //    which keep streaming into the loop below.
+  constexpr int kBatch = 4;
+  const int chunks_per_row = spad * 8; // 16-byte chunks of x
+  const int xtotal = M * chunks_per_row;
+  const int stotal = kWaves * 32 * gr;
+  auto load_x = [&](int base, u32x4 (&v)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int c = base + j * kThreads;
       const int m = c / chunks_per_row;
-      const int q = c - m * chunks_per_row;
-      const u32x4 v = Load8<XDT>::get(x + int64_t(m) * ldx + int64_t(s_begin) * 64 + 8 * q);
-      *reinterpret_cast<u32x4 *>(xl + m * xs_stride + 8 * q) = v;
+      const int qk = c - m * chunks_per_row;
+      v[j] = u32x4{0u, 0u, 0u, 0u};
+      if (c < xtotal && qk < ns * 8)
+        v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + int64_t(s0) * 64 + 8 * qk);
     }
+  };
+  auto store_x = [&](int base, const u32x4 (&v)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int c = base + j * kThreads;
+      const int m = c / chunks_per_row;
+      const int qk = c - m * chunks_per_row;
+      if (c < xtotal)
+        *reinterpret_cast<u32x4 *>(xl + m * xs_stride + 8 * qk) = BITS == 4 ? even_odd(v[j]) : v[j];
+    }
+  };
+  // Consecutive threads read consecutive groups of a row; groups past the
+  // last one repeat it (their x is zero).
+  auto load_s = [&](int base, float2 (&sb)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int e = min(base + j * kThreads, stotal - 1);
+      const int wv = e / (32 * gr);
+      const int rem = e - wv * 32 * gr;
+      const int row = rem / gr;
+      const int g = min(g0 + (rem - row * gr), groups - 1);
+      int n = (blockIdx.x * kWaves + wv) * 32 + row;
+      n = n < N ? n : N - 1;
+      const int64_t gi = int64_t(n) * groups + g;
+      sb[j].x = Elem<SDT>::load(scales[gi]);
+      sb[j].y = Elem<SDT>::load(biases[gi]);
+    }
+  };
+  auto store_s = [&](int base, const float2 (&sb)[kBatch]) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int e = base + j * kThreads;
+      if (e < stotal) *reinterpret_cast<float2 *>(sbl + 2 * e) = sb[j];
+    }
+  };
+  {
+    u32x4 xv[kBatch];
+    float2 sv[kBatch];
+    load_x(tid, xv);
+    load_s(tid, sv);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_chunk(d, q[d]);
+    store_x(tid, xv);
+    store_s(tid, sv);
+  }
+  for (int base = tid + kThreads * kBatch; base < xtotal; base += kThreads * kBatch) {
+    u32x4 xv[kBatch];
+    load_x(base, xv);
+    store_x(base, xv);
+  }
+  for (int base = tid + kThreads * kBatch; base < stotal; base += kThreads * kBatch) {
+    float2 sv[kBatch];
+    load_s(base, sv);
+    store_s(base, sv);
   }
   __syncthreads();
-  // 3. Per-step sums of the staged values (dot2 against (1, 1)); rows >= M
+  // 2. Per-step sums of the staged values (dot2 against (1, 1)); rows >= M
   //    are zero.
   {
     const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
-    for (int p = tid; p < ns * MROWS; p += kThreads) {
+    for (int p = tid; p < spad * MROWS; p += kThreads) {
       const int sl = p / MROWS;
       const int m = p - sl * MROWS;
       float sum = 0.0f;
@@ -188,113 +278,160 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(
     }
   }
   __syncthreads();
+  if (!live) return; // no further block-wide synchronisation
 
-  // 4. The queue's steps.
+  // 3. Stream the chunks.
+  const uint16_t *arow = xl + (r < M ? r : M - 1) * xs_stride + 32 * h;
+  const float *sbrow = sbl + 2 * (wave * 32 + r) * gr;
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 
-  auto compute = [&](const Stage<BITS> &st, int sl, float weight) {
-    const uint16_t *ap = arow + sl * 64;
-    floatx16 t;
+  auto compute_chunk = [&](const u32x4 (&cq)[4], int c) {
+    // Turn the chunk around through the wave's buffer: written as eight
+    // rows per load, read back as this lane's row r, half h.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = 0.0f;
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4 *>(wbuf + (8 * i + (lane >> 3)) * kWRow + 16 * (lane & 7)) = cq[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    u32x4 bw[kC][BITS / 4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 a = *reinterpret_cast<const u32x4 *>(ap + 8 * i);
-      u32x4 bq;
-      if constexpr (BITS == 4) {
-        bq = codes4_plus128(st.w[0][i]);
-      } else {
-        bq = codes8(st.w[i / 2][(i % 2) * 2], st.w[i / 2][(i % 2) * 2 + 1]);
+    for (int u = 0; u < kC; ++u)
+#pragma unroll
+      for (int v = 0; v < BITS / 4; ++v)
+        bw[u][v] = *reinterpret_cast<const u32x4 *>(wbuf + r * kWRow + u * kStepBytes +
+                                                    h * (kStepBytes / 2) + 16 * v);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int u = 0; u < kC; ++u) {
+      const int sl = c * kC + u; // local step; past the range the staged x is zero
+      const uint16_t *ap = arow + sl * 64;
+      floatx16 t;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t[i] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(ap + 8 * i);
+        u32x4 bq;
+        if constexpr (BITS == 4) {
+          bq = codes4_plus128(bw[u][0][i]);
+        } else {
+          bq = codes8(bw[u][i / 2][(i % 2) * 2], bw[u][i / 2][(i % 2) * 2 + 1]);
+        }
+        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), t, 0, 0, 0);
       }
-      t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), t, 0, 0, 0);
-    }
-    const float sv = st.s * weight;
-    const float cv = (st.b - kOff * st.s) * weight;
-    const float *xs_step = xsum + sl * MROWS;
+      const int g = min(((s0 + sl) * 64) / GS - g0, gr - 1);
+      const float2 sb = *reinterpret_cast<const float2 *>(sbrow + 2 * g);
+      const float sv = sb.x;
+      const float cv = sb.y - kOff * sb.x;
+      const float *xs_step = xsum + sl * MROWS;
 #pragma unroll
-    for (int j = 0; j < kAcc / 4; ++j) {
-      const floatx4 xs = *reinterpret_cast<const floatx4 *>(xs_step + 8 * j + 4 * h);
+      for (int j = 0; j < kAcc / 4; ++j) {
+        const floatx4 xs = *reinterpret_cast<const floatx4 *>(xs_step + 8 * j + 4 * h);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[4 * j + e] = fmaf(sv, t[4 * j + e], acc[4 * j + e]);
-        acc[4 * j + e] = fmaf(cv, xs[e], acc[4 * j + e]);
+        for (int e = 0; e < 4; ++e) {
+          acc[4 * j + e] = fmaf(sv, t[4 * j + e], acc[4 * j + e]);
+          acc[4 * j + e] = fmaf(cv, xs[e], acc[4 * j + e]);
+        }
       }
     }
   };
 
-  for (int base = 0; base < my_steps; base += kDepth) {
+  // Each slot is refilled with the chunk kDepth later as soon as it has been
+  // used.
+  for (int base = 0; base < nchunks; base += kDepth) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
-      const int i = base + d;
-      compute(q[d], local_step(i), i < my_steps ? 1.0f : 0.0f);
+      const int c = base + d;
+      if (c < nchunks) compute_chunk(q[d], c);
       __builtin_amdgcn_sched_barrier(0);
-      load_stage(local_step(i + kDepth), q[d]);
+      load_chunk(c + kDepth, q[d]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // 5. Sum the waves.  Accumulator entry i of lane (r, h) is row
-  //    8*(i/4) + 4*h + i%4, column r.  `red` reuses the staging space.
-  __syncthreads();
+  // 4. Accumulator entry i of lane (r, h) is token 8*(i/4) + 4*h + i%4,
+  //    weight row r of the tile.
+  const int n = tile * 32 + r;
+  if (nsplit == 1) {
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) {
+      const int m = 8 * (i / 4) + 4 * h + (i % 4);
+      if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(acc[i]);
+    }
+    return;
+  }
+  // K was split: this wave's partial tile goes out as agent-scope stores,
+  // which do not stay in this XCD's L2; once they have completed the wave
+  // counts itself in, and the last wave of the tile adds every split's
+  // partial in split order and re-arms the counter.
+  float *mine = partial + ((int64_t(split) * tiles + tile) * MROWS) * 32;
 #pragma unroll
   for (int i = 0; i < kAcc; ++i) {
     const int m = 8 * (i / 4) + 4 * h + (i % 4);
-    red[(wave * MROWS + m) * 32 + r] = acc[i];
+    __hip_atomic_store(mine + m * 32 + r, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  for (int o = tid; o < MROWS * 32; o += kThreads) {
-    const int m = o >> 5;
-    const int c = o & 31;
-    const int nn = tile * 32 + c;
-    if (m < M && nn < N) {
-      float v = red[m * 32 + c];
-#pragma unroll
-      for (int wv = 1; wv < kWaves; ++wv) v += red[(wv * MROWS + m) * 32 + c];
-      if (nsplit == 1)
-        y[int64_t(m) * N + nn] = Elem<ODT>::store(v);
-      else
-        __hip_atomic_store(&partial[(int64_t(split) * M + m) * N + nn], v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (nsplit == 1) return;
-
-  // 6. K was split.  The partials went out as agent-scope stores, which do
-  //    not stay in this XCD's L2; wait until they have completed, then count
-  //    this split in.  The last block to arrive reads every split's partial
-  //    with agent-scope loads, adds them in split order and re-arms the
-  //    counter for the next call.
-  __shared__ unsigned s_last;
   __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's stores are done
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == unsigned(nsplit - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (int o = tid; o < MROWS * 32; o += kThreads) {
-    const int m = o >> 5;
-    const int c = o & 31;
-    const int nn = tile * 32 + c;
-    if (m < M && nn < N) {
-      float v = 0.0f;
-      for (int sp = 0; sp < nsplit; ++sp)
-        v += __hip_atomic_load(&partial[(int64_t(sp) * M + m) * N + nn], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      y[int64_t(m) * N + nn] = Elem<ODT>::store(v);
+  unsigned prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  if (prev != unsigned(nsplit - 1)) return;
+  // The partials of kSplitBatch splits are loaded together (one round trip
+  // per batch rather than per value), then added in split order.
+  constexpr int kSplitBatch = 4;
+  float v[kAcc];
+#pragma unroll
+  for (int i = 0; i < kAcc; ++i) v[i] = 0.0f;
+  for (int sp0 = 0; sp0 < nsplit; sp0 += kSplitBatch) {
+    float t[kSplitBatch][kAcc];
+#pragma unroll
+    for (int j = 0; j < kSplitBatch; ++j) {
+      const int sp = min(sp0 + j, nsplit - 1);
+      const float *src = partial + ((int64_t(sp) * tiles + tile) * MROWS) * 32 + r;
+#pragma unroll
+      for (int i = 0; i < kAcc; ++i)
+        t[j][i] = __hip_atomic_load(src + (8 * (i / 4) + 4 * h + (i % 4)) * 32, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
     }
+#pragma unroll
+    for (int j = 0; j < kSplitBatch; ++j)
+      if (sp0 + j < nsplit)
+#pragma unroll
+        for (int i = 0; i < kAcc; ++i) v[i] += t[j][i];
   }
-  if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int i = 0; i < kAcc; ++i) {
+    const int m = 8 * (i / 4) + 4 * h + (i % 4);
+    if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(v[i]);
+  }
+  if (lane == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-size_t qmv_lds_bytes(int M, int mrows, int steps_per_split) {
-  const size_t staged = size_t(M) * x_stride(steps_per_split) * 2 + size_t(steps_per_split) * mrows * 4;
-  const size_t reduce = size_t(kWaves) * mrows * 32 * 4;
-  return std::max(staged, reduce);
+// Groups a range of `steps` 64-wide steps can touch (one more when a
+// 128-group range starts mid-group).
+__host__ __device__ inline int range_groups(int steps, int gs) { return (steps * 64) / gs + 1; }
+
+template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS, int WAVES, int DEPTH>
+void launch_qmv_w(void *y, const void *x, int64_t ldx, const uint32_t *w,
+                  const void *s, const void *b, int M, int N, int K,
+                  const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
+                  hipStream_t st) {
+  const int tiles = (N + 31) / 32;
+  const dim3 grid((tiles + WAVES - 1) / WAVES, plan.splits);
+  const int sps = plan.groups_per_split;
+  const int spad = (sps + chunk_steps(BITS) - 1) / chunk_steps(BITS) * chunk_steps(BITS);
+  const int gr = range_groups(spad, GS);
+  const QmvLds l = qmv_lds(WAVES, M, MROWS, spad, gr);
+  if (l.total > kLdsBudget) fail("qmv: plan exceeds the LDS budget");
+  qmv_kernel<BITS, XDT, SDT, ODT, MROWS, GS, WAVES, DEPTH><<<grid, 64 * WAVES, l.total, st>>>(
+      static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
+      w, static_cast<const typename Elem<SDT>::T *>(s),
+      static_cast<const typename Elem<SDT>::T *>(b), M, N, K, sps, gr, ws.partial, ws.counters);
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS>
@@ -302,14 +439,8 @@ void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K,
                   const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
                   hipStream_t st) {
-  const dim3 grid((N + 31) / 32, plan.splits);
-  const size_t lds = qmv_lds_bytes(M, MROWS, plan.groups_per_split);
-  if (lds > 64 * 1024) fail("qmv: plan exceeds the LDS budget");
-  qmv_kernel<BITS, XDT, SDT, ODT, MROWS, GS><<<grid, kThreads, lds, st>>>(
-      static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
-      w, static_cast<const typename Elem<SDT>::T *>(s),
-      static_cast<const typename Elem<SDT>::T *>(b), M, N, K, plan.groups_per_split,
-      ws.partial, ws.counters);
+  if (plan.waves != 4) fail("qmv: plan must use four waves per block");
+  launch_qmv_w<BITS, XDT, SDT, ODT, MROWS, GS, 4, 4>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
 }
 
 template <int BITS, int XDT, int SDT, int ODT>
@@ -317,13 +448,19 @@ void launch_qmv_m(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
                   const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
                   hipStream_t st) {
+  // MROWS: the token rows the kernel keeps (the accumulator holds MROWS / 2
+  // entries per lane).
   if (gs == 64) {
-    if (M <= 16)
+    if (M <= 8)
+      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+    else if (M <= 16)
       launch_qmv_t<BITS, XDT, SDT, ODT, 16, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
     else
       launch_qmv_t<BITS, XDT, SDT, ODT, 32, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
   } else {
-    if (M <= 16)
+    if (M <= 8)
+      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+    else if (M <= 16)
       launch_qmv_t<BITS, XDT, SDT, ODT, 16, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
     else
       launch_qmv_t<BITS, XDT, SDT, ODT, 32, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
@@ -346,33 +483,40 @@ void launch_qmv_m(void *y, const void *x, int64_t ldx, const uint32_t *w,
 
 namespace kern {
 
-QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int cus) {
-  (void)group_size;
+QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus) {
   QmvPlan p;
   const int64_t steps = K / 64;
   const int64_t tiles = (N + 31) / 32;
-  const int64_t mrows = M <= 16 ? 16 : 32;
-  // Split K only when there are fewer 32-row tiles than CUs: a split adds a
-  // round trip (partials, counter, reload) that these short kernels feel.
-  const int64_t target_blocks = int64_t(cus > 0 ? cus : 256);
-  int64_t splits = (target_blocks + tiles - 1) / tiles;
-  // At least one step per wave ...
-  splits = std::min<int64_t>(splits, std::max<int64_t>(1, steps / kWaves));
-  // ... and a K range whose rows of x fit the LDS budget.
-  int64_t max_steps = (kXBudget / (2 * M) - 8) / 64;
-  max_steps = std::max<int64_t>(1, std::min<int64_t>(max_steps, 1024));
-  while (size_t(M) * x_stride(int(max_steps)) * 2 + size_t(max_steps) * mrows * 4 > size_t(kXBudget) + 8192 &&
-         max_steps > 1)
-    --max_steps;
-  splits = std::max<int64_t>(splits, (steps + max_steps - 1) / max_steps);
-  if (splits < 1) splits = 1;
+  const int mrows = M <= 8 ? 8 : M <= 16 ? 16 : 32;
+  const int c = chunk_steps(bits);
+  const int64_t ncu = cus > 0 ? cus : 256;
+  auto fits = [&](int waves, int64_t s) {
+    const int pad = int((s + c - 1) / c * c);
+    return qmv_lds(waves, int(M), mrows, pad, range_groups(pad, group_size)).total <= kLdsBudget;
+  };
+  auto finish = [&](int waves, int64_t sps) {
+    sps = std::min<int64_t>(sps, steps);
+    const int64_t splits = (steps + sps - 1) / sps;
+    p.waves = waves;
+    p.splits = int(splits);
+    p.groups_per_split = int(sps);
+    p.partial_floats = splits > 1 ? size_t(splits) * size_t(tiles) * size_t(mrows) * 32 : 0;
+    p.counters = int(tiles);
+    return p;
+  };
+  // Four waves per block and K split so that there are about two blocks per
+  // CU, in ranges of whole chunks that fit the LDS: many short ranges keep
+  // more bytes in flight than a few long ones, which outweighs the partial
+  // round trips at the end.
+  // (Rounded down: a grid just over two blocks per CU would need a second
+  // round wherever a third block does not fit.)
+  const int64_t tile_groups = (tiles + 3) / 4;
+  const int64_t target = 2 * ncu;
+  int64_t splits = std::max<int64_t>(1, target / tile_groups);
   int64_t sps = (steps + splits - 1) / splits;
-  splits = (steps + sps - 1) / sps;
-  p.splits = int(splits);
-  p.groups_per_split = int(sps);
-  p.partial_floats = splits > 1 ? size_t(splits) * size_t(M) * size_t(N) : 0;
-  p.counters = int(tiles);
-  return p;
+  sps = (sps + c - 1) / c * c;
+  while (sps > c && !fits(4, sps)) sps -= c;
+  return finish(4, sps);
 }
 
 void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
@@ -386,6 +530,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
   if (K % group_size != 0) fail("qmv: K % group_size != 0");
   if (bits != 4 && bits != 8) fail("qmv: bits must be 4 or 8");
   if (ldx < K || ldx % 8 != 0) fail("qmv: row stride of x must be >= K and a multiple of 8");
+  if (N * K * bits / 8 >= (int64_t(1) << 31)) fail("qmv: the packed weight must be under 2 GiB");
   if (plan.splits < 1 || plan.groups_per_split < 1 ||
       int64_t(plan.splits) * plan.groups_per_split < K / 64 ||
       int64_t(plan.splits - 1) * plan.groups_per_split >= K / 64)

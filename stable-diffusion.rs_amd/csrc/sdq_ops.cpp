@@ -96,7 +96,7 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
   if (bits != 4 && bits != 8)
     fail("the quantized matmul kernels take 4 or 8 bits, got " + std::to_string(bits));
   if (M <= 32) {
-    kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, cu_count(device));
+    kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, bits, cu_count(device));
     kern::SplitWorkspace ws;
     if (plan.splits > 1) {
       *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
