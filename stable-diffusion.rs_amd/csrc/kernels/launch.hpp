@@ -22,8 +22,9 @@ void dequantize(const uint32_t *wq, const void *scales, const void *biases,
                 int bits, void *out, int out_dtype, hipStream_t stream);
 
 // Workspace the matmul kernels use when they split K across blocks: partial
-// tiles and one counter per split tile.  The counters must be zero on entry;
-// the kernels leave them zero.
+// tiles, and for qmv one counter per split tile (zero on entry; the kernel
+// leaves them zero).  qmm adds its partials in a second kernel and needs no
+// counters.
 struct SplitWorkspace {
   float *partial = nullptr;
   unsigned *counters = nullptr;
@@ -56,7 +57,6 @@ struct QmmPlan {
   int steps_per_split = 0;  // 64-wide K steps per range
   int blocks = 0;           // grid size
   size_t partial_floats = 0; // workspace needed (0 without split tiles)
-  int counters = 0;         // split tiles
 };
 
 // y [M, N] = x [M, K] @ dequantize(w).T for any M.  qmm.hip.

@@ -67,14 +67,14 @@ __device__ __forceinline__ u32x4 dequant8<8>(const u32x4 (&wr)[2], int i, float 
 // Work assignment of one launch.  Tiles are numbered M-tile major; tiles
 // [0, dp_tiles) are computed whole, one block each; each tile after that is
 // split into `splits` K ranges of `steps_per_split` 64-wide steps, one block
-// per range, reduced through `partial` and `counters`.
+// per range, each writing its f32 partial tile to `partial`
+// ([split tile][range][BM][256], row-major); qmm_reduce_kernel adds them.
 struct QmmWork {
   int tiles_n;
   int dp_tiles;
   int splits;
   int steps_per_split;
   float *partial;
-  unsigned *counters;
 };
 
 template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH>
@@ -432,52 +432,20 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   };
 
   if (bid >= wk.dp_tiles) {
-    // A K range of a split tile.  Its accumulators go out as agent-scope
-    // (L2-bypassing) stores, register-major so that each store instruction
-    // writes 256 consecutive floats; once they have completed the block
-    // counts itself in.  The last block of the tile to arrive reads every
-    // range's partial back with agent-scope loads (its own from registers),
-    // adds them in range order -- the same order whichever block is last, so
-    // the result is deterministic -- re-arms the counter and stores the tile.
-    const int sk = tile - wk.dp_tiles;
-    constexpr int kRegs = MB * 2 * 16;
-    float *base = wk.partial + int64_t(sk) * wk.splits * (kRegs * kThreads) + tid;
-    float *mine = base + int64_t(split) * (kRegs * kThreads);
+    // A K range of a split tile: its f32 accumulators go to the workspace
+    // register-major (entry ((mb*2 + j)*16 + e) of thread t at float
+    // ((mb*2 + j)*16 + e)*256 + t of the range's slot), so that each store
+    // instruction writes 256 consecutive bytes per wave; rows past M are
+    // written too and never read.  The reduction kernel that follows on the
+    // stream adds the ranges in order.
+    const int64_t slot = int64_t(tile - wk.dp_tiles) * wk.splits + split;
+    float *mine = wk.partial + slot * (BM * kTileN) + tid;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          __hip_atomic_store(mine + ((mb * 2 + j) * 16 + e) * kThreads, acc[mb][j][e],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __shared__ unsigned s_last;
-    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's stores are done
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(&wk.counters[sk], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      s_last = prev == unsigned(wk.splits - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // The sums go straight to the output: writing them back into the
-    // accumulators would make the register allocator copy accumulators
-    // inside the main loop.
-    store_tile([&](int mb, int j, float (&sum)[16]) {
-      for (int p = 0; p < wk.splits; ++p) {
-        const float *src = base + int64_t(p) * (kRegs * kThreads) + ((mb * 2 + j) * 16) * kThreads;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float t = p == split ? acc[mb][j][e]
-                                     : __hip_atomic_load(src + e * kThreads, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-          sum[e] = p == 0 ? t : sum[e] + t;
-        }
-      }
-    });
-    if (tid == 0)
-      __hip_atomic_store(&wk.counters[sk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int e = 0; e < 16; ++e) mine[((mb * 2 + j) * 16 + e) * kThreads] = acc[mb][j][e];
     return;
   }
 
@@ -487,12 +455,70 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   });
 }
 
+// Sum of the K ranges of the split tiles, in range order (so the result does
+// not depend on which block finished first), converted to the output type.
+// Thread t of the launch handles four consecutive floats of the
+// register-major partial layout: threads 4c..4c+3 of one MFMA tile entry,
+// i.e. four consecutive columns of one output row.
+template <int ODT>
+__global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
+                                                         const float *__restrict__ partial,
+                                                         int M, int N, int bm, int tiles_n,
+                                                         int dp_tiles, int splits) {
+  using OT = typename Elem<ODT>::T;
+  const int per_tile = bm * (kTileN / 4); // float4 pieces of one partial tile
+  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int sk = int(idx / per_tile);
+  const int within = int(idx % per_tile);
+  const int reg = within / (kThreads / 4);       // (mb*2 + j)*16 + e
+  const int t = 4 * (within % (kThreads / 4));  // first of four threads
+  const int lane = t & 63, wave = t >> 6;
+  const int mb = reg >> 5, j = (reg >> 4) & 1, e = reg & 15;
+  const int row = 32 * mb + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+  const int col = wave * 64 + 32 * j + (lane & 31);
+  const int tile = dp_tiles + sk;
+  const int grow = (tile / tiles_n) * bm + row;
+  const int gcol = (tile % tiles_n) * kTileN + col;
+  if (grow >= M || gcol >= N) return;
+  const float4 *src = reinterpret_cast<const float4 *>(partial) + int64_t(sk) * splits * per_tile + within;
+  float4 sum = src[0];
+  for (int p0 = 1; p0 < splits; p0 += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (p0 + q < splits) v[q] = src[int64_t(p0 + q) * per_tile];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (p0 + q < splits) {
+        sum.x += v[q].x;
+        sum.y += v[q].y;
+        sum.z += v[q].z;
+        sum.w += v[q].w;
+      }
+  }
+  OT *d = y + int64_t(grow) * N + gcol;
+  const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+  if (gcol + 4 <= N && (reinterpret_cast<uintptr_t>(d) % (4 * sizeof(OT))) == 0) {
+    if constexpr (sizeof(OT) == 4) {
+      *reinterpret_cast<float4 *>(d) = sum;
+    } else {
+      uint2 v;
+      v.x = uint32_t(Elem<ODT>::store(s4[0])) | (uint32_t(Elem<ODT>::store(s4[1])) << 16);
+      v.y = uint32_t(Elem<ODT>::store(s4[2])) | (uint32_t(Elem<ODT>::store(s4[3])) << 16);
+      *reinterpret_cast<uint2 *>(d) = v;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (gcol + q < N) d[q] = Elem<ODT>::store(s4[q]);
+  }
+}
+
 template <int BITS, int XDT, int SDT, int ODT, int BM>
 void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws, hipStream_t st) {
-  const QmmWork wk{plan.tiles_n, plan.dp_tiles, plan.splits, plan.steps_per_split, ws.partial,
-                   ws.counters};
+  const QmmWork wk{plan.tiles_n, plan.dp_tiles, plan.splits, plan.steps_per_split, ws.partial};
   const dim3 grid(plan.blocks);
   auto *yp = static_cast<typename Elem<ODT>::T *>(y);
   auto *xp = static_cast<const typename Elem<XDT>::T *>(x);
@@ -512,6 +538,13 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
     else SDQ_QMM_LAUNCH(128, false);
   }
 #undef SDQ_QMM_LAUNCH
+  const int sk_tiles = plan.tiles - plan.dp_tiles;
+  if (sk_tiles > 0) {
+    hip_check(hipGetLastError(), "qmm launch");
+    const int64_t threads = int64_t(sk_tiles) * BM * (kTileN / 4);
+    qmm_reduce_kernel<ODT><<<dim3(unsigned(threads / 256)), 256, 0, st>>>(
+        yp, ws.partial, M, N, BM, plan.tiles_n, plan.dp_tiles, plan.splits);
+  }
 }
 
 template <int BITS, int XDT, int SDT, int ODT>
@@ -548,22 +581,25 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
   p.tiles = int(tiles_m * p.tiles_n);
   const int64_t steps = K / 64;
   const int64_t slots = cus > 0 ? cus : 256; // one block per CU at a time
-  const int64_t rounds = p.tiles / slots;
   const int64_t rem = p.tiles % slots;
   // The last, partly filled round of whole tiles costs as much as a full
   // one.  Its tiles can instead be split along K into ranges that run side
-  // by side; each range then costs its length in steps, plus about one step
-  // per range for writing and re-reading its partial tile.
+  // by side.  Costs in thousandths of a 64-wide step of one block: a range
+  // costs its length, plus a fixed part (writing its partial tile, and the
+  // reduction kernel's launch), plus its share of the reduction kernel,
+  // which reads every partial tile once at roughly HBM speed.
+  constexpr int64_t kSplitFixed = 4000;
+  constexpr int64_t kReducePerRange = 45;
   p.dp_tiles = p.tiles;
   p.splits = 1;
   p.steps_per_split = int(steps);
   if (rem > 0) {
-    int64_t best = steps;
+    int64_t best = steps * 1000;
     for (int64_t s = 2; s <= 16 && rem * s <= slots; ++s) {
       const int64_t sps = (steps + s - 1) / s;
-      if (sps < 4) break;
+      if (sps < 2) break;
       const int64_t ranges = (steps + sps - 1) / sps;
-      const int64_t cost = sps + ranges;
+      const int64_t cost = sps * 1000 + kSplitFixed + rem * ranges * kReducePerRange;
       if (cost < best) {
         best = cost;
         p.splits = int(ranges);
@@ -575,7 +611,6 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
   const int64_t sk_tiles = p.tiles - p.dp_tiles;
   p.blocks = int(p.dp_tiles + sk_tiles * p.splits);
   p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * size_t(p.bm) * kTileN;
-  p.counters = int(sk_tiles);
   return p;
 }
 
@@ -606,7 +641,7 @@ void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
        (int64_t(plan.splits - 1) * plan.steps_per_split >= K / 64 ||
         int64_t(plan.splits) * plan.steps_per_split < K / 64)))
     fail("qmm: inconsistent launch plan");
-  if (plan.dp_tiles < plan.tiles && (!ws.partial || !ws.counters))
+  if (plan.dp_tiles < plan.tiles && !ws.partial)
     fail("qmm: split-K launch without a workspace");
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_FLOAT32, SDQ_FLOAT32)
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_BFLOAT16, SDQ_BFLOAT16)

@@ -111,7 +111,6 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
     if (plan.dp_tiles < plan.tiles) {
       *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
       ws.partial = static_cast<float *>((*keep_alive)->ptr);
-      ws.counters = split_counters(device, stream, plan.counters);
     }
     kern::qmm(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
               plan, ws, stream);

@@ -131,8 +131,8 @@ def test_split_k_is_deterministic_and_correct(oracle, sdq, stream, M):
 ])
 def test_large_m_split_k_is_deterministic_and_correct(oracle, sdq, stream, M, N, K, bits):
     # When the tiles do not fill whole rounds of CUs, the MFMA kernel splits
-    # the tiles of the last round along K; the last block of each such tile
-    # adds the partials in range order, so repeated calls agree bit for bit.
+    # the tiles of the last round along K; a second kernel adds the ranges'
+    # partial tiles in range order, so repeated calls agree bit for bit.
     print(f"qmm split-K M={M} N={N} K={K} bits={bits}", flush=True)
     q, deq = _qweight(oracle, sdq, stream, 930 + M + bits, N, K, bits)
     x_dev, x_vals = _x(oracle, sdq, 931 + M, (M, K), "bf16")
