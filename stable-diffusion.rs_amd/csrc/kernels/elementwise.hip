@@ -48,21 +48,62 @@ __global__ __launch_bounds__(kThreads) void binary_kernel(const typename Elem<A>
 
 // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), the operation order
 // of mlx.rs:1048-1053.
-template <int D>
-__global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::T *__restrict__ a,
-                                                        typename Elem<D>::T *__restrict__ out,
-                                                        int64_t n) {
+// 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), through the identity
+// 1 + tanh(u) = 2 (1 - r) for u >= 0 and 2 r' for u < 0, with
+// r = 1 / (1 + exp(2|u|)): each branch keeps full relative precision (no
+// cancellation near tanh = -1), exp from the hardware base-2 exponential
+// and the reciprocal from the hardware reciprocal (both about 1 ulp).  The
+// result stays within 5e-7 of the f32 formula with a correctly rounded tanh
+// for |v| <= 8, and saturates cleanly (exp overflows to inf, r to 0).
+__device__ __forceinline__ float gelu_approx_f(float v) {
   // sqrt(2 / pi) as the reference evaluates it in f32: sqrtf(2.0f / PI_f32),
   // one ulp below the correctly rounded constant.
   const float c = 0.7978845238685608f;
   const float k = 0.044715f;
+  const float kTwoLog2e = 2.8853900817779268f; // 2 / ln 2
+  const float u = (v + ((v * v) * v) * k) * c;
+  const float e = __builtin_amdgcn_exp2f(fabsf(u) * kTwoLog2e);
+  const float r = __builtin_amdgcn_rcpf(e + 1.0f);
+  return u >= 0.0f ? v * (1.0f - r) : v * r;
+}
+
+// Eight elements per thread with 16-byte accesses where both pointers allow
+// (the launch checks), the ragged tail one element per thread.
+template <int D>
+__global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::T *__restrict__ a,
+                                                        typename Elem<D>::T *__restrict__ out,
+                                                        int64_t n, bool vec) {
+  using T = typename Elem<D>::T;
+  constexpr int kWords = int(sizeof(T)) * 8 / 4; // 32-bit words per 8 elements
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-    const float v = Elem<D>::load(a[i]);
-    const float cubed = (v * v) * v;
-    const float inner = tanhf((v + cubed * k) * c);
-    out[i] = Elem<D>::store((v * 0.5f) * (inner + 1.0f));
+  const int64_t tid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t groups = vec ? n / 8 : 0;
+  for (int64_t g = tid; g < groups; g += stride) {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a + g * 8);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(out + g * 8);
+    u32x4 w[kWords / 4];
+#pragma unroll
+    for (int q = 0; q < kWords / 4; ++q) w[q] = __builtin_nontemporal_load(src + q);
+#pragma unroll
+    for (int q = 0; q < kWords / 4; ++q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t word = w[q][j];
+        if constexpr (sizeof(T) == 4) {
+          w[q][j] = __float_as_uint(gelu_approx_f(__uint_as_float(word)));
+        } else {
+          const float lo = Elem<D>::load(T(word & 0xffffu));
+          const float hi = Elem<D>::load(T(word >> 16));
+          w[q][j] = uint32_t(Elem<D>::store(gelu_approx_f(lo))) |
+                    (uint32_t(Elem<D>::store(gelu_approx_f(hi))) << 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kWords / 4; ++q) __builtin_nontemporal_store(w[q], dst + q);
   }
+  for (int64_t i = groups * 8 + tid; i < n; i += stride)
+    out[i] = Elem<D>::store(gelu_approx_f(Elem<D>::load(a[i])));
 }
 
 #define SDQ_FLOAT_DISPATCH(dt, NAME, ...)                                    \
@@ -131,11 +172,14 @@ void multiply(const void *a, int a_dtype, const void *b, int b_dtype,
 void gelu_approx(const void *a, int dtype, void *out, int64_t n,
                  hipStream_t stream) {
   if (n == 0) return;
-  const int grid = grid_for(n);
+  const bool vec = reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  // A few groups of eight per thread keep many loads in flight without a
+  // huge grid.
+  const int grid = grid_for((vec ? n / 8 : n) / 4 + 1);
   SDQ_FLOAT_DISPATCH(dtype, D, {
     gelu_kernel<D><<<grid, kThreads, 0, stream>>>(
         static_cast<const typename Elem<D>::T *>(a),
-        static_cast<typename Elem<D>::T *>(out), n);
+        static_cast<typename Elem<D>::T *>(out), n, vec);
   });
   hip_check(hipGetLastError(), "gelu launch");
 }

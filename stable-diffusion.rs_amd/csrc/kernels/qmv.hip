@@ -177,79 +177,59 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
 
   // 1. Stage x[0:M, s0*64 : (s0+spad)*64] as bf16, zero past the range (at
   //    4 bits each eight elements in the codes' even/odd order), and the
-  //    waves' scales and biases, kBatch loads per thread at a time.  The
-  //    first batch's loads go out before the wave's first kDepth code chunks
-  //    and are stored after them: the wait for the staging then does not
-  //    include the chunks (loads complete in issue order for the counter),
-  //    which keep streaming into the loop below.
-  constexpr int kBatch = 4;
+  //    waves' scales and biases.  Every staging load goes out in one batch,
+  //    before the wave's first kDepth code chunks, and is stored after them:
+  //    the wait for the staging then does not include the chunks (loads
+  //    complete in issue order for the counter), which keep streaming into
+  //    the loop below.  The plan keeps a range short enough for one batch:
+  //    kXB 16-byte pieces of x and kSB scale/bias pairs per thread.
+  constexpr int kXB = MROWS / 2;
+  constexpr int kSB = 8;
   const int chunks_per_row = spad * 8; // 16-byte chunks of x
   const int xtotal = M * chunks_per_row;
   const int stotal = kWaves * 32 * gr;
-  auto load_x = [&](int base, u32x4 (&v)[kBatch]) {
+  u32x4 xv[kXB];
+  float2 sv[kSB];
+  // Pieces past the range or past x are loaded from a valid address and
+  // replaced by zeros, so every load is unconditional.
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int c = base + j * kThreads;
-      const int m = c / chunks_per_row;
-      const int qk = c - m * chunks_per_row;
-      v[j] = u32x4{0u, 0u, 0u, 0u};
-      if (c < xtotal && qk < ns * 8)
-        v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + int64_t(s0) * 64 + 8 * qk);
-    }
-  };
-  auto store_x = [&](int base, const u32x4 (&v)[kBatch]) {
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int c = base + j * kThreads;
-      const int m = c / chunks_per_row;
-      const int qk = c - m * chunks_per_row;
-      if (c < xtotal)
-        *reinterpret_cast<u32x4 *>(xl + m * xs_stride + 8 * qk) = BITS == 4 ? even_odd(v[j]) : v[j];
-    }
-  };
+  for (int j = 0; j < kXB; ++j) {
+    const int c = min(tid + j * kThreads, xtotal - 1);
+    const int m = c / chunks_per_row;
+    const int qk = min(c - m * chunks_per_row, ns * 8 - 1);
+    xv[j] = Load8<XDT>::get(x + int64_t(m) * ldx + int64_t(s0) * 64 + 8 * qk);
+  }
   // Consecutive threads read consecutive groups of a row; groups past the
   // last one repeat it (their x is zero).
-  auto load_s = [&](int base, float2 (&sb)[kBatch]) {
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int e = min(base + j * kThreads, stotal - 1);
-      const int wv = e / (32 * gr);
-      const int rem = e - wv * 32 * gr;
-      const int row = rem / gr;
-      const int g = min(g0 + (rem - row * gr), groups - 1);
-      int n = (blockIdx.x * kWaves + wv) * 32 + row;
-      n = n < N ? n : N - 1;
-      const int64_t gi = int64_t(n) * groups + g;
-      sb[j].x = Elem<SDT>::load(scales[gi]);
-      sb[j].y = Elem<SDT>::load(biases[gi]);
-    }
-  };
-  auto store_s = [&](int base, const float2 (&sb)[kBatch]) {
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int e = base + j * kThreads;
-      if (e < stotal) *reinterpret_cast<float2 *>(sbl + 2 * e) = sb[j];
-    }
-  };
-  {
-    u32x4 xv[kBatch];
-    float2 sv[kBatch];
-    load_x(tid, xv);
-    load_s(tid, sv);
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) load_chunk(d, q[d]);
-    store_x(tid, xv);
-    store_s(tid, sv);
+  for (int j = 0; j < kSB; ++j) {
+    const int e = min(tid + j * kThreads, stotal - 1);
+    const int wv = e / (32 * gr);
+    const int rem = e - wv * 32 * gr;
+    const int row = rem / gr;
+    const int g = min(g0 + (rem - row * gr), groups - 1);
+    int n = (blockIdx.x * kWaves + wv) * 32 + row;
+    n = n < N ? n : N - 1;
+    const int64_t gi = int64_t(n) * groups + g;
+    sv[j].x = Elem<SDT>::load(scales[gi]);
+    sv[j].y = Elem<SDT>::load(biases[gi]);
   }
-  for (int base = tid + kThreads * kBatch; base < xtotal; base += kThreads * kBatch) {
-    u32x4 xv[kBatch];
-    load_x(base, xv);
-    store_x(base, xv);
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) load_chunk(d, q[d]);
+#pragma unroll
+  for (int j = 0; j < kXB; ++j) {
+    const int c = tid + j * kThreads;
+    const int m = c / chunks_per_row;
+    const int qk = c - m * chunks_per_row;
+    if (c < xtotal) {
+      const u32x4 v = qk < ns * 8 ? xv[j] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4 *>(xl + m * xs_stride + 8 * qk) = BITS == 4 ? even_odd(v) : v;
+    }
   }
-  for (int base = tid + kThreads * kBatch; base < stotal; base += kThreads * kBatch) {
-    float2 sv[kBatch];
-    load_s(base, sv);
-    store_s(base, sv);
+#pragma unroll
+  for (int j = 0; j < kSB; ++j) {
+    const int e = tid + j * kThreads;
+    if (e < stotal) *reinterpret_cast<float2 *>(sbl + 2 * e) = sv[j];
   }
   __syncthreads();
   // 2. Per-step sums of the staged values (dot2 against (1, 1)); rows >= M
@@ -306,24 +286,31 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // The kC steps' products are independent: their MFMAs are interleaved so
+    // that none waits for the previous one's result.
+    floatx16 t[kC];
 #pragma unroll
-    for (int u = 0; u < kC; ++u) {
-      const int sl = c * kC + u; // local step; past the range the staged x is zero
-      const uint16_t *ap = arow + sl * 64;
-      floatx16 t;
+    for (int u = 0; u < kC; ++u)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) t[i] = 0.0f;
+      for (int e = 0; e < 16; ++e) t[u][e] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(ap + 8 * i);
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int u = 0; u < kC; ++u) {
+        // Local step c*kC + u; past the range the staged x is zero.
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(arow + (c * kC + u) * 64 + 8 * i);
         u32x4 bq;
         if constexpr (BITS == 4) {
           bq = codes4_plus128(bw[u][0][i]);
         } else {
           bq = codes8(bw[u][i / 2][(i % 2) * 2], bw[u][i / 2][(i % 2) * 2 + 1]);
         }
-        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), t, 0, 0, 0);
+        t[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), t[u], 0, 0, 0);
       }
+    }
+#pragma unroll
+    for (int u = 0; u < kC; ++u) {
+      const int sl = c * kC + u;
       const int g = min(((s0 + sl) * 64) / GS - g0, gr - 1);
       const float2 sb = *reinterpret_cast<const float2 *>(sbrow + 2 * g);
       const float sv = sb.x;
@@ -334,7 +321,7 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
         const floatx4 xs = *reinterpret_cast<const floatx4 *>(xs_step + 8 * j + 4 * h);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[4 * j + e] = fmaf(sv, t[4 * j + e], acc[4 * j + e]);
+          acc[4 * j + e] = fmaf(sv, t[u][4 * j + e], acc[4 * j + e]);
           acc[4 * j + e] = fmaf(cv, xs[e], acc[4 * j + e]);
         }
       }
@@ -416,6 +403,11 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
 // 128-group range starts mid-group).
 __host__ __device__ inline int range_groups(int steps, int gs) { return (steps * 64) / gs + 1; }
 
+// Longest K range (64-wide steps, a multiple of both chunk sizes) whose
+// staging fits the kernel's single batch: at most 16 steps of x and 16
+// groups of scales and biases per row.
+inline int max_range_steps(int gs) { return gs == 64 ? 12 : 16; }
+
 template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS, int WAVES, int DEPTH>
 void launch_qmv_w(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K,
@@ -428,6 +420,9 @@ void launch_qmv_w(void *y, const void *x, int64_t ldx, const uint32_t *w,
   const int gr = range_groups(spad, GS);
   const QmvLds l = qmv_lds(WAVES, M, MROWS, spad, gr);
   if (l.total > kLdsBudget) fail("qmv: plan exceeds the LDS budget");
+  // The staging is one batch per thread: MROWS/2 pieces of x, 8 scale pairs.
+  if (spad > 16 || M * spad * 8 > (MROWS / 2) * 64 * WAVES || WAVES * 32 * gr > 8 * 64 * WAVES)
+    fail("qmv: K range too long for the staging batch");
   qmv_kernel<BITS, XDT, SDT, ODT, MROWS, GS, WAVES, DEPTH><<<grid, 64 * WAVES, l.total, st>>>(
       static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
       w, static_cast<const typename Elem<SDT>::T *>(s),
@@ -515,6 +510,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
   int64_t splits = std::max<int64_t>(1, target / tile_groups);
   int64_t sps = (steps + splits - 1) / splits;
   sps = (sps + c - 1) / c * c;
+  sps = std::min<int64_t>(sps, max_range_steps(group_size));
   while (sps > c && !fits(4, sps)) sps -= c;
   return finish(4, sps);
 }

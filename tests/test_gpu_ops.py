@@ -16,6 +16,21 @@ def test_gelu_approx_matches_the_oracle(oracle, sdq, stream):
     assert np.max(np.abs(got - oracle.gelu_approx(x))) < 2e-6
 
 
+@pytest.mark.parametrize("n", [1, 7, 8, 4096 + 5])
+def test_gelu_approx_bf16_and_ragged_lengths(oracle, sdq, stream, n):
+    # bf16 in and out, 16-byte groups of eight plus a ragged tail: within the
+    # f32 bound of the test above plus one bf16 rounding of the output, against
+    # the oracle applied to the same (bf16) inputs.
+    x = (oracle.normals(5 + n, n) * 3).astype(np.float32)
+    bits = sdq.f32_to_bf16_bits(x)
+    xr = sdq.bf16_bits_to_f32(bits)
+    got = sdq.bf16_bits_to_f32(sdq.Array.from_numpy(bits, sdq.BFLOAT16).gelu_approx(stream).to_numpy())
+    want = oracle.gelu_approx(xr)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 2e-6)
+    f = sdq.Array.from_numpy(x).gelu_approx(stream).to_numpy()
+    assert np.max(np.abs(f - oracle.gelu_approx(x))) < 2e-6
+
+
 def test_astype_round_trips(oracle, sdq, stream):
     x = oracle.normals(4, 4096)
     a = sdq.Array.from_numpy(x)
