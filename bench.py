@@ -65,12 +65,20 @@ def measured_traffic(label):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # The GPU's clocks ramp over the first ~100-150 steps (~40 ms) after idle:
+    # per-step time falls from ~340 to ~277 us.  The warmup covers the ramp.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--rotate", type=int, default=10, help="distinct weight copies (>= 9 exceeds the MALL)")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline work")
+    ap.add_argument("--unfused", action="store_true",
+                    help="time the step with GELU as its own kernel between the two matmuls (the reference's "
+                         "sequence of calls) instead of fused into fc1's epilogue; the other form is timed "
+                         "and reported beside it either way")
+    ap.add_argument("--no-compare", action="store_true",
+                    help="skip timing the other GELU form (keeps a profiler's trace to one form)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, run one f32->bf16 copy of 2^27 elements (512 MiB read, "
                          "256 MiB written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -97,12 +105,17 @@ class Layer:
         return sum(c.resident_bytes() for c in self.copies)
 
 
-def launch(L, layer, copy, y_ptr, x_ptr, M, hstream, sdq):
+def launch(L, layer, copy, y_ptr, x_ptr, M, hstream, sdq, act=0):
     w, s, b = layer.ptrs[copy % len(layer.ptrs)]
-    rc = L.sdq_quantized_matmul_raw(y_ptr, sdq.BFLOAT16, x_ptr, sdq.BFLOAT16, layer.K, w, s, b,
-                                    sdq.FLOAT32, M, layer.N, layer.K, GS, layer.bits, hstream)
+    if act:
+        rc = L.sdq_quantized_matmul_epilogue_raw(y_ptr, sdq.BFLOAT16, x_ptr, sdq.BFLOAT16, layer.K, w, s, b,
+                                                 sdq.FLOAT32, M, layer.N, layer.K, GS, layer.bits, None, 0,
+                                                 act, hstream)
+    else:
+        rc = L.sdq_quantized_matmul_raw(y_ptr, sdq.BFLOAT16, x_ptr, sdq.BFLOAT16, layer.K, w, s, b,
+                                        sdq.FLOAT32, M, layer.N, layer.K, GS, layer.bits, hstream)
     if rc:
-        sdq._check(rc, "quantized_matmul_raw")
+        sdq._check(rc, "quantized_matmul")
 
 
 def cpu_baseline(args, fc1, fc2):
@@ -172,15 +185,22 @@ def main():
     ts = torch.cuda.current_stream()
     hs = ts.cuda_stream
 
-    def step(i, ev=None):
+    def step(i, ev=None, fused=not args.unfused):
+        # fused: GELU in fc1's epilogue (sdq_quantized_matmul_epilogue_raw);
+        # unfused: fc1, then the GELU kernel, then fc2 (the reference's
+        # sequence of calls, flux.rs:400-413).
         if ev:
             ev[0].record(ts)
-        launch(L, fc1, i, h.data_ptr(), x.data_ptr(), M_TOKENS, hs, sdq)
+        if fused:
+            launch(L, fc1, i, a.data_ptr(), x.data_ptr(), M_TOKENS, hs, sdq, act=sdq.ACT_GELU_APPROX)
+        else:
+            launch(L, fc1, i, h.data_ptr(), x.data_ptr(), M_TOKENS, hs, sdq)
         if ev:
             ev[1].record(ts)
-        rc = L.sdq_gelu_approx_raw(a.data_ptr(), h.data_ptr(), sdq.BFLOAT16, h.numel(), hs)
-        if rc:
-            sdq._check(rc, "gelu_approx_raw")
+        if not fused:
+            rc = L.sdq_gelu_approx_raw(a.data_ptr(), h.data_ptr(), sdq.BFLOAT16, h.numel(), hs)
+            if rc:
+                sdq._check(rc, "gelu_approx_raw")
         if ev:
             ev[2].record(ts)
         launch(L, fc2, i, y.data_ptr(), a.data_ptr(), M_TOKENS, hs, sdq)
@@ -206,6 +226,19 @@ def main():
     for i in range(args.steps):
         step(args.warmup + args.steps + i, evs[i])
     torch.cuda.synchronize()
+    # The other form of the step, timed the same way, for comparison.
+    other_ms = float("nan")
+    if not args.no_compare:
+        for i in range(args.warmup):
+            step(i, fused=args.unfused)
+        o_start, o_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        o_start.record(ts)
+        for i in range(args.steps):
+            step(args.warmup + i, fused=args.unfused)
+        o_end.record(ts)
+        torch.cuda.synchronize()
+        other_ms = o_start.elapsed_time(o_end) / args.steps
     if args.copy_probe:
         src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
         dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
@@ -222,15 +255,17 @@ def main():
     flops_fc2 = 2.0 * M_TOKENS * MLP * HIDDEN
     flops_step = flops_fc1 + flops_fc2
     value = flops_step / (ms_step / 1e3) / 1e12
-    log(f"step {ms_step:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms): fc1 {k_fc1:.3f} ms "
+    form, other_form = ("unfused", "fused") if args.unfused else ("fused", "unfused")
+    log(f"step {ms_step:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms, GELU {form}): fc1 {k_fc1:.3f} ms "
         f"({flops_fc1 / k_fc1 / 1e9:.0f} TFLOP/s), gelu {k_gelu:.3f} ms, fc2 {k_fc2:.3f} ms "
-        f"({flops_fc2 / k_fc2 / 1e9:.0f} TFLOP/s)")
+        f"({flops_fc2 / k_fc2 / 1e9:.0f} TFLOP/s); {other_form} step {other_ms:.3f} ms")
 
     # Dominant kernel's roofline (MFMA-bound at M = 1536: AI far above the ridge).
     # One call is the tile kernel plus, when the plan splits K, the reduction
     # kernel of its partial tiles; the events bracket the whole call.
     if k_fc1 >= k_fc2:
-        dom, dom_ms, dom_flops, dom_layer, label = ("qmm fc1 4-bit 1536x3072->12288 (qmm_kernel + qmm_reduce_kernel)",
+        epi = "" if args.unfused else ", GELU epilogue"
+        dom, dom_ms, dom_flops, dom_layer, label = (f"qmm fc1 4-bit 1536x3072->12288 (qmm_kernel + qmm_reduce_kernel{epi})",
                                                     k_fc1, flops_fc1, fc1, "fc1")
     else:
         dom, dom_ms, dom_flops, dom_layer, label = ("qmm fc2 8-bit 1536x12288->3072 (qmm_kernel + qmm_reduce_kernel)",
@@ -308,7 +343,10 @@ def main():
             "seq_len": M_TOKENS,
             "parallelism": "single GPU",
             "weight_copies_rotated": args.rotate,
+            "gelu": "separate kernel between the matmuls (sdq_gelu_approx_raw)" if args.unfused else
+                    "fused into fc1's epilogue (sdq_quantized_matmul_epilogue_raw)",
         },
+        f"ms_per_step_{other_form}": None if args.no_compare else round(other_ms, 4),
         "kernels_ms": {"fc1": round(k_fc1, 4), "gelu": round(k_gelu, 4), "fc2": round(k_fc2, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -204,6 +204,27 @@ int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w,
                          sdq_optional_int group_size, sdq_optional_int bits,
                          const char *mode, sdq_stream s);
 
+/* Activations the matmul epilogue can apply. */
+typedef enum sdq_activation_ {
+  SDQ_ACT_NONE = 0,
+  SDQ_ACT_GELU_APPROX = 1, /* Array::gelu_approx (mlx.rs:1041-1054) */
+} sdq_activation;
+
+/* quantized::linear's quantized branch (quantized.rs:293-318) with its bias
+ * add, plus an optional activation, fused into the matmul's store:
+ * y = act(x @ dequantize(w).T + bias).  It replaces the call sequence
+ * mlx_quantized_matmul (quantized.rs:305-306) -> mlx_add (314-317) and, for
+ * the Flux MLP, -> gelu_approx (flux.rs:400-413); the reference has no single
+ * mlx-c call for it.  bias: a float array of N values, or a handle whose ctx
+ * is NULL for none.  The sum and the activation are computed in f32 from the
+ * f32 accumulator and rounded once to y's dtype (the unfused sequence rounds
+ * after each op, so the two can differ by an output rounding step).  Other
+ * arguments and errors as sdq_quantized_matmul with transpose = true. */
+int sdq_quantized_linear(sdq_array *res, sdq_array x, sdq_array w,
+                         sdq_array scales, sdq_array biases, sdq_array bias,
+                         int activation, sdq_optional_int group_size,
+                         sdq_optional_int bits, const char *mode, sdq_stream s);
+
 /* ---- elementwise ops the linear and its callers use ------------------------- */
 
 /* replaces mlx_add (mlx.rs:124) for the shapes the quantized linear needs:
@@ -240,6 +261,19 @@ int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype,
                              const void *scales, const void *biases,
                              int s_dtype, int64_t M, int64_t N, int64_t K,
                              int group_size, int bits, void *hip_stream);
+
+/* sdq_quantized_matmul_raw with sdq_quantized_linear's epilogue:
+ * y = act(x @ dequantize(w).T + bias) on caller-owned device memory.  bias:
+ * N values of bias_dtype (float32/bfloat16/float16), or NULL for none;
+ * activation: an sdq_activation. */
+int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x,
+                                      int x_dtype, int64_t ldx,
+                                      const uint32_t *w, const void *scales,
+                                      const void *biases, int s_dtype,
+                                      int64_t M, int64_t N, int64_t K,
+                                      int group_size, int bits,
+                                      const void *bias, int bias_dtype,
+                                      int activation, void *hip_stream);
 
 /* tanh-GELU on caller-owned device memory (dtype float32/bfloat16/float16),
  * enqueued on `hip_stream`: the elementwise step between the two Flux MLP

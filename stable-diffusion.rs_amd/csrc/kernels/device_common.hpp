@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "sdq.h"
+#include "launch.hpp"
 
 namespace sdq {
 namespace dev {
@@ -185,6 +186,39 @@ template <> struct BLoad8<SDQ_FLOAT32> {
     return o;
   }
 };
+
+// 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), through the identity
+// 1 + tanh(u) = 2 (1 - r) for u >= 0 and 2 r' for u < 0, with
+// r = 1 / (1 + exp(2|u|)): each branch keeps full relative precision (no
+// cancellation near tanh = -1), exp from the hardware base-2 exponential
+// and the reciprocal from the hardware reciprocal (both about 1 ulp).  The
+// result stays within 5e-7 of the f32 formula with a correctly rounded tanh
+// for |v| <= 8, and saturates cleanly (exp overflows to inf, r to 0).
+__device__ __forceinline__ float gelu_approx_f(float v) {
+  // sqrt(2 / pi) as the reference evaluates it in f32: sqrtf(2.0f / PI_f32),
+  // one ulp below the correctly rounded constant.
+  const float c = 0.7978845238685608f;
+  const float k = 0.044715f;
+  const float kTwoLog2e = 2.8853900817779268f; // 2 / ln 2
+  const float u = (v + ((v * v) * v) * k) * c;
+  const float e = __builtin_amdgcn_exp2f(fabsf(u) * kTwoLog2e);
+  const float r = __builtin_amdgcn_rcpf(e + 1.0f);
+  return u >= 0.0f ? v * (1.0f - r) : v * r;
+}
+
+// The matmul epilogue (kern::Epilogue) on one f32 result: bias of output
+// column n, then the activation; the caller rounds once to the output dtype.
+__device__ __forceinline__ float epi_bias(const kern::Epilogue &ep, int64_t n) {
+  if (!ep.bias) return 0.0f;
+  if (ep.bias_dtype == SDQ_FLOAT32) return static_cast<const float *>(ep.bias)[n];
+  const uint16_t h = static_cast<const uint16_t *>(ep.bias)[n];
+  return ep.bias_dtype == SDQ_BFLOAT16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+__device__ __forceinline__ float epi_apply(const kern::Epilogue &ep, float v, float bias) {
+  v += bias;
+  return ep.act == 1 ? gelu_approx_f(v) : v;
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
   return __builtin_bit_cast(bf16x8, v);

@@ -48,25 +48,6 @@ __global__ __launch_bounds__(kThreads) void binary_kernel(const typename Elem<A>
 
 // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), the operation order
 // of mlx.rs:1048-1053.
-// 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), through the identity
-// 1 + tanh(u) = 2 (1 - r) for u >= 0 and 2 r' for u < 0, with
-// r = 1 / (1 + exp(2|u|)): each branch keeps full relative precision (no
-// cancellation near tanh = -1), exp from the hardware base-2 exponential
-// and the reciprocal from the hardware reciprocal (both about 1 ulp).  The
-// result stays within 5e-7 of the f32 formula with a correctly rounded tanh
-// for |v| <= 8, and saturates cleanly (exp overflows to inf, r to 0).
-__device__ __forceinline__ float gelu_approx_f(float v) {
-  // sqrt(2 / pi) as the reference evaluates it in f32: sqrtf(2.0f / PI_f32),
-  // one ulp below the correctly rounded constant.
-  const float c = 0.7978845238685608f;
-  const float k = 0.044715f;
-  const float kTwoLog2e = 2.8853900817779268f; // 2 / ln 2
-  const float u = (v + ((v * v) * v) * k) * c;
-  const float e = __builtin_amdgcn_exp2f(fabsf(u) * kTwoLog2e);
-  const float r = __builtin_amdgcn_rcpf(e + 1.0f);
-  return u >= 0.0f ? v * (1.0f - r) : v * r;
-}
-
 // Eight elements per thread with 16-byte accesses where both pointers allow
 // (the launch checks), the ragged tail one element per thread.
 template <int D>

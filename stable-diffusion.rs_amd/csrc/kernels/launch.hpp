@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "sdq.h"
+
 namespace sdq {
 namespace kern {
 
@@ -20,6 +22,24 @@ void quantize(const void *w, int w_dtype, int64_t rows, int64_t cols,
 void dequantize(const uint32_t *wq, const void *scales, const void *biases,
                 int s_dtype, int64_t rows, int64_t cols, int group_size,
                 int bits, void *out, int out_dtype, hipStream_t stream);
+
+// Output epilogue of the matmul kernels, applied to each f32 result before
+// its one rounding to the output dtype: y = act(acc + bias[n]).  `bias` is a
+// device pointer to N values (null: none) of `bias_dtype` (float32, bfloat16
+// or float16); act 0 = none, 1 = tanh-GELU.  It composes the bias add after
+// the quantized matmul (quantized.rs:314-317) and the GELU after the Flux
+// MLP's first linear (flux.rs:400-413) into the matmul's store.
+struct Epilogue {
+  const void *bias = nullptr;
+  int bias_dtype = 0;
+  int act = 0;
+};
+
+inline bool epilogue_ok(const Epilogue &ep) {
+  const bool dt = ep.bias_dtype == SDQ_FLOAT32 || ep.bias_dtype == SDQ_BFLOAT16 ||
+                  ep.bias_dtype == SDQ_FLOAT16;
+  return (ep.bias == nullptr || dt) && (ep.act == 0 || ep.act == 1);
+}
 
 // Workspace the matmul kernels use when they split K across blocks: partial
 // tiles, and for qmv one counter per split tile (zero on entry; the kernel
@@ -44,7 +64,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
          int bits, const QmvPlan &plan, const SplitWorkspace &ws,
-         hipStream_t stream);
+         const Epilogue &ep, hipStream_t stream);
 
 // Tile and split-K plan of one qmm launch (a pure function of the shape and
 // the CU count).
@@ -64,7 +84,8 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus);
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, const QmmPlan &plan, const SplitWorkspace &ws, hipStream_t stream);
+         int bits, const QmmPlan &plan, const SplitWorkspace &ws, const Epilogue &ep,
+         hipStream_t stream);
 
 // Elementwise helpers (elementwise.hip).  n = element count.
 void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
     const typename Elem<SDT>::T *__restrict__ scales,
-    const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, QmmWork wk) {
+    const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, QmmWork wk,
+    kern::Epilogue ep) {
   using XT = typename Elem<XDT>::T;
   using ST = typename Elem<SDT>::T;
   constexpr int MB = BM / 32;           // 32-row MFMA blocks per wave
@@ -449,9 +450,14 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     return;
   }
 
+  // The epilogue needs only the column's bias: one value per lane per 32-row
+  // block of weights.
+  float bcol[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
   store_tile([&](int mb, int j, float (&v)[16]) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) v[e] = acc[mb][j][e];
+    for (int e = 0; e < 16; ++e) v[e] = epi_apply(ep, acc[mb][j][e], bcol[j]);
   });
 }
 
@@ -464,7 +470,8 @@ template <int ODT>
 __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
                                                          const float *__restrict__ partial,
                                                          int M, int N, int bm, int tiles_n,
-                                                         int dp_tiles, int splits) {
+                                                         int dp_tiles, int splits,
+                                                         kern::Epilogue ep) {
   using OT = typename Elem<ODT>::T;
   const int per_tile = bm * (kTileN / 4); // float4 pieces of one partial tile
   const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -497,10 +504,12 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
       }
   }
   OT *d = y + int64_t(grow) * N + gcol;
-  const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+  float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) s4[q] = epi_apply(ep, s4[q], epi_bias(ep, min(gcol + q, N - 1)));
   if (gcol + 4 <= N && (reinterpret_cast<uintptr_t>(d) % (4 * sizeof(OT))) == 0) {
     if constexpr (sizeof(OT) == 4) {
-      *reinterpret_cast<float4 *>(d) = sum;
+      *reinterpret_cast<float4 *>(d) = float4{s4[0], s4[1], s4[2], s4[3]};
     } else {
       uint2 v;
       v.x = uint32_t(Elem<ODT>::store(s4[0])) | (uint32_t(Elem<ODT>::store(s4[1])) << 16);
@@ -517,7 +526,8 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
 template <int BITS, int XDT, int SDT, int ODT, int BM>
 void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
-                  const kern::QmmPlan &plan, const kern::SplitWorkspace &ws, hipStream_t st) {
+                  const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
+                  const kern::Epilogue &ep, hipStream_t st) {
   const QmmWork wk{plan.tiles_n, plan.dp_tiles, plan.splits, plan.steps_per_split, ws.partial};
   const dim3 grid(plan.blocks);
   auto *yp = static_cast<typename Elem<ODT>::T *>(y);
@@ -529,7 +539,7 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
   const bool sch = srow_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(s) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(b) % 16 == 0;
 #define SDQ_QMM_LAUNCH(G, C) \
-  qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk)
+  qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk, ep)
   if (gs == 64) {
     if (sch) SDQ_QMM_LAUNCH(64, true);
     else SDQ_QMM_LAUNCH(64, false);
@@ -543,28 +553,29 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
     hip_check(hipGetLastError(), "qmm launch");
     const int64_t threads = int64_t(sk_tiles) * BM * (kTileN / 4);
     qmm_reduce_kernel<ODT><<<dim3(unsigned(threads / 256)), 256, 0, st>>>(
-        yp, ws.partial, M, N, BM, plan.tiles_n, plan.dp_tiles, plan.splits);
+        yp, ws.partial, M, N, BM, plan.tiles_n, plan.dp_tiles, plan.splits, ep);
   }
 }
 
 template <int BITS, int XDT, int SDT, int ODT>
 void launch_qmm_bm(void *y, const void *x, int64_t ldx, const uint32_t *w,
                    const void *s, const void *b, int M, int N, int K, int gs,
-                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws, hipStream_t st) {
+                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
+                   const kern::Epilogue &ep, hipStream_t st) {
   if (plan.bm == 128)
-    launch_qmm_t<BITS, XDT, SDT, ODT, 128>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, st);
+    launch_qmm_t<BITS, XDT, SDT, ODT, 128>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
   else
-    launch_qmm_t<BITS, XDT, SDT, ODT, 256>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, st);
+    launch_qmm_t<BITS, XDT, SDT, ODT, 256>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
 }
 
 #define SDQ_QMM_CASE(XD, SD, OD)                                                         \
   if (x_dtype == XD && s_dtype == SD && y_dtype == OD) {                                 \
     if (bits == 4)                                                                       \
       launch_qmm_bm<4, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K),  \
-                                   group_size, plan, ws, stream);                        \
+                                   group_size, plan, ws, ep, stream);                    \
     else                                                                                 \
       launch_qmm_bm<8, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K),  \
-                                   group_size, plan, ws, stream);                        \
+                                   group_size, plan, ws, ep, stream);                    \
     hip_check(hipGetLastError(), "qmm launch");                                          \
     return;                                                                              \
   }
@@ -617,7 +628,8 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, const QmmPlan &plan, const SplitWorkspace &ws, hipStream_t stream) {
+         int bits, const QmmPlan &plan, const SplitWorkspace &ws, const Epilogue &ep,
+         hipStream_t stream) {
   if (M < 1 || N < 1 || K < 64 || K % 64 != 0) fail("qmm: bad M, N or K");
   if (M > (int64_t(1) << 30) || N > (int64_t(1) << 30) || K > (int64_t(1) << 30))
     fail("qmm: dimension too large");
@@ -643,6 +655,7 @@ void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
     fail("qmm: inconsistent launch plan");
   if (plan.dp_tiles < plan.tiles && !ws.partial)
     fail("qmm: split-K launch without a workspace");
+  if (!kern::epilogue_ok(ep)) fail("qmm: bad epilogue (bias dtype or activation)");
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_FLOAT32, SDQ_FLOAT32)
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_BFLOAT16, SDQ_BFLOAT16)
   SDQ_QMM_CASE(SDQ_FLOAT32, SDQ_FLOAT32, SDQ_FLOAT32)

@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
     const typename Elem<SDT>::T *__restrict__ scales,
     const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K,
     int steps_per_split, int groups_range, float *__restrict__ partial,
-    unsigned *__restrict__ counters) {
+    unsigned *__restrict__ counters, kern::Epilogue ep) {
   constexpr int kWaves = WAVES;
   constexpr int kThreads = 64 * WAVES;
   constexpr int kDepth = DEPTH;
@@ -345,10 +345,11 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
   //    weight row r of the tile.
   const int n = tile * 32 + r;
   if (nsplit == 1) {
+    const float bn = epi_bias(ep, min(n, N - 1));
 #pragma unroll
     for (int i = 0; i < kAcc; ++i) {
       const int m = 8 * (i / 4) + 4 * h + (i % 4);
-      if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(acc[i]);
+      if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(epi_apply(ep, acc[i], bn));
     }
     return;
   }
@@ -391,10 +392,11 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
 #pragma unroll
         for (int i = 0; i < kAcc; ++i) v[i] += t[j][i];
   }
+  const float bn = epi_bias(ep, min(n, N - 1));
 #pragma unroll
   for (int i = 0; i < kAcc; ++i) {
     const int m = 8 * (i / 4) + 4 * h + (i % 4);
-    if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(v[i]);
+    if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(epi_apply(ep, v[i], bn));
   }
   if (lane == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -412,7 +414,7 @@ template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS, int WAVES, int
 void launch_qmv_w(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K,
                   const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
-                  hipStream_t st) {
+                  const kern::Epilogue &ep, hipStream_t st) {
   const int tiles = (N + 31) / 32;
   const dim3 grid((tiles + WAVES - 1) / WAVES, plan.splits);
   const int sps = plan.groups_per_split;
@@ -426,39 +428,39 @@ void launch_qmv_w(void *y, const void *x, int64_t ldx, const uint32_t *w,
   qmv_kernel<BITS, XDT, SDT, ODT, MROWS, GS, WAVES, DEPTH><<<grid, 64 * WAVES, l.total, st>>>(
       static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
       w, static_cast<const typename Elem<SDT>::T *>(s),
-      static_cast<const typename Elem<SDT>::T *>(b), M, N, K, sps, gr, ws.partial, ws.counters);
+      static_cast<const typename Elem<SDT>::T *>(b), M, N, K, sps, gr, ws.partial, ws.counters, ep);
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int MROWS, int GS>
 void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K,
                   const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
-                  hipStream_t st) {
+                  const kern::Epilogue &ep, hipStream_t st) {
   if (plan.waves != 4) fail("qmv: plan must use four waves per block");
-  launch_qmv_w<BITS, XDT, SDT, ODT, MROWS, GS, 4, 4>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+  launch_qmv_w<BITS, XDT, SDT, ODT, MROWS, GS, 4, 4>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
 }
 
 template <int BITS, int XDT, int SDT, int ODT>
 void launch_qmv_m(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
                   const kern::QmvPlan &plan, const kern::SplitWorkspace &ws,
-                  hipStream_t st) {
+                  const kern::Epilogue &ep, hipStream_t st) {
   // MROWS: the token rows the kernel keeps (the accumulator holds MROWS / 2
   // entries per lane).
   if (gs == 64) {
     if (M <= 8)
-      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
     else if (M <= 16)
-      launch_qmv_t<BITS, XDT, SDT, ODT, 16, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 16, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
     else
-      launch_qmv_t<BITS, XDT, SDT, ODT, 32, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 32, 64>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
   } else {
     if (M <= 8)
-      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 8, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
     else if (M <= 16)
-      launch_qmv_t<BITS, XDT, SDT, ODT, 16, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 16, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
     else
-      launch_qmv_t<BITS, XDT, SDT, ODT, 32, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, st);
+      launch_qmv_t<BITS, XDT, SDT, ODT, 32, 128>(y, x, ldx, w, s, b, M, N, K, plan, ws, ep, st);
   }
 }
 
@@ -466,10 +468,10 @@ void launch_qmv_m(void *y, const void *x, int64_t ldx, const uint32_t *w,
   if (x_dtype == XD && s_dtype == SD && y_dtype == OD) {                              \
     if (bits == 4)                                                                    \
       launch_qmv_m<4, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K), \
-                                  group_size, plan, ws, stream);                      \
+                                  group_size, plan, ws, ep, stream);                  \
     else                                                                              \
       launch_qmv_m<8, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K), \
-                                  group_size, plan, ws, stream);                      \
+                                  group_size, plan, ws, ep, stream);                  \
     hip_check(hipGetLastError(), "qmv launch");                                       \
     return;                                                                           \
   }
@@ -519,7 +521,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
          int bits, const QmvPlan &plan, const SplitWorkspace &ws,
-         hipStream_t stream) {
+         const Epilogue &ep, hipStream_t stream) {
   if (M < 1 || M > 32) fail("qmv: M must be in [1, 32]");
   if (N < 1 || K < 64 || K % 64 != 0) fail("qmv: bad N or K");
   if (group_size != 64 && group_size != 128) fail("qmv: group size must be 64 or 128");
@@ -532,6 +534,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
       int64_t(plan.splits - 1) * plan.groups_per_split >= K / 64)
     fail("qmv: inconsistent plan");
   if (plan.splits > 1 && (!ws.partial || !ws.counters)) fail("qmv: split without workspace");
+  if (!epilogue_ok(ep)) fail("qmv: bad epilogue (bias dtype or activation)");
   SDQ_QMV_CASE(SDQ_BFLOAT16, SDQ_FLOAT32, SDQ_FLOAT32)
   SDQ_QMV_CASE(SDQ_BFLOAT16, SDQ_BFLOAT16, SDQ_BFLOAT16)
   SDQ_QMV_CASE(SDQ_FLOAT32, SDQ_FLOAT32, SDQ_FLOAT32)

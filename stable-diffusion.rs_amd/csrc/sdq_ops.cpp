@@ -89,7 +89,7 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
                      const uint32_t *w, const void *scales, const void *biases,
                      int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
                      int device, hipStream_t stream,
-                     std::shared_ptr<Buffer> *keep_alive) {
+                     std::shared_ptr<Buffer> *keep_alive, const kern::Epilogue &ep = {}) {
   if (M == 0 || N == 0) return;
   if (gs != 64 && gs != 128)
     fail("the quantized matmul kernels take group size 64 or 128, got " + std::to_string(gs));
@@ -104,7 +104,7 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
       ws.counters = split_counters(device, stream, plan.counters);
     }
     kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ws, stream);
+              plan, ws, ep, stream);
   } else {
     kern::QmmPlan plan = kern::plan_qmm(M, N, K, cu_count(device));
     kern::SplitWorkspace ws;
@@ -113,7 +113,7 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
       ws.partial = static_cast<float *>((*keep_alive)->ptr);
     }
     kern::qmm(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ws, stream);
+              plan, ws, ep, stream);
   }
 }
 
@@ -217,10 +217,16 @@ int sdq_dequantize(sdq_array *res, sdq_array w, sdq_array scales, sdq_array bias
   });
 }
 
-int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
-                         sdq_array biases, bool transpose, sdq_optional_int group_size,
-                         sdq_optional_int bits, const char *mode, sdq_stream s) {
-  SDQ_GUARD("quantized_matmul", {
+} // extern "C"
+
+namespace {
+
+// quantized_matmul with an optional output epilogue (bias [N], activation),
+// shared by sdq_quantized_matmul and sdq_quantized_linear.
+void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                           sdq_array biases, bool transpose, sdq_optional_int group_size,
+                           sdq_optional_int bits, const char *mode, sdq_stream s,
+                           sdq_array bias, int activation) {
     StreamImpl *st = stream_of(s, "quantized_matmul");
     check_mode(mode, sdq_array{nullptr});
     const int gs = opt_or(group_size, 64);
@@ -258,7 +264,22 @@ int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w, sdq_array sca
       fail("Last dimension of first input with shape " + shape_str(xa->shape) +
            " must match the dequantized weight's input width " + std::to_string(K) +
            " (weight " + shape_str(wa->shape) + ", bits=" + std::to_string(nb) + ")");
+    kern::Epilogue ep;
+    ArrayImpl *bb = nullptr;
+    if (bias.ctx) {
+      bb = array_of(bias, "quantized_linear", "bias");
+      same_device(bb, st, "bias");
+      if (!is_float_dtype(bb->dtype) || bb->size != size_t(N) || (!bb->shape.empty() && bb->shape.back() != N))
+        fail("bias must be a float array of shape [" + std::to_string(N) + "], got " +
+             shape_str(bb->shape) + " " + dtype_name(bb->dtype));
+      ep.bias = bb->data();
+      ep.bias_dtype = bb->dtype;
+    }
+    if (activation != SDQ_ACT_NONE && activation != SDQ_ACT_GELU_APPROX)
+      fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(activation));
+    ep.act = activation;
     const int out_dtype = promote_float(xa->dtype, sa->dtype);
+    if (bb) order_after(bb, st);
     order_after(xa, st);
     order_after(wa, st);
     order_after(sa, st);
@@ -270,10 +291,34 @@ int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w, sdq_array sca
     std::shared_ptr<Buffer> scratch;
     matmul_dispatch(out->data(), out_dtype, xa->data(), xa->dtype, K,
                     static_cast<const uint32_t *>(wa->data()), sa->data(), ba->data(), sa->dtype,
-                    M, N, K, gs, nb, st->device, st->stream, &scratch);
+                    M, N, K, gs, nb, st->device, st->stream, &scratch, ep);
     set_result(res, std::move(out));
+}
+
+} // namespace
+
+extern "C" {
+
+int sdq_quantized_matmul(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                         sdq_array biases, bool transpose, sdq_optional_int group_size,
+                         sdq_optional_int bits, const char *mode, sdq_stream s) {
+  SDQ_GUARD("quantized_matmul", {
+    quantized_matmul_impl(res, x, w, scales, biases, transpose, group_size, bits, mode, s,
+                          sdq_array{nullptr}, SDQ_ACT_NONE);
   });
 }
+
+int sdq_quantized_linear(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                         sdq_array biases, sdq_array bias, int activation,
+                         sdq_optional_int group_size, sdq_optional_int bits, const char *mode,
+                         sdq_stream s) {
+  SDQ_GUARD("quantized_linear", {
+    quantized_matmul_impl(res, x, w, scales, biases, true, group_size, bits, mode, s, bias,
+                          activation);
+  });
+}
+
+
 
 int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
                              const uint32_t *w, const void *scales, const void *biases,
@@ -291,6 +336,34 @@ int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, i
     std::shared_ptr<Buffer> scratch;
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
                     group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch);
+  });
+}
+
+int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x, int x_dtype,
+                                      int64_t ldx, const uint32_t *w, const void *scales,
+                                      const void *biases, int s_dtype, int64_t M, int64_t N,
+                                      int64_t K, int group_size, int bits, const void *bias,
+                                      int bias_dtype, int activation, void *hip_stream) {
+  SDQ_GUARD("quantized_matmul_epilogue_raw", {
+    if (M < 0 || N < 0 || K <= 0) fail("M, N must be >= 0 and K > 0");
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(s_dtype) || !is_float_dtype(y_dtype))
+      fail("dtypes must be float32, bfloat16 or float16");
+    if (bias && !is_float_dtype(bias_dtype))
+      fail("bias dtype must be float32, bfloat16 or float16");
+    if (activation != SDQ_ACT_NONE && activation != SDQ_ACT_GELU_APPROX)
+      fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(activation));
+    check_group_bits(group_size, bits);
+    if (K % group_size != 0) fail("K must be a multiple of group_size");
+    if (M > 0 && N > 0 && (!y || !x || !w || !scales || !biases)) fail("NULL pointer argument");
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    kern::Epilogue ep;
+    ep.bias = bias;
+    ep.bias_dtype = bias ? bias_dtype : 0;
+    ep.act = activation;
+    std::shared_ptr<Buffer> scratch;
+    matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch, ep);
   });
 }
 

@@ -38,6 +38,8 @@ __all__ = [
     "BFLOAT16",
     "FLOAT16",
     "UINT32",
+    "ACT_NONE",
+    "ACT_GELU_APPROX",
     "f32_to_bf16_bits",
     "bf16_bits_to_f32",
 ]
@@ -48,6 +50,9 @@ LIB_PATH = Path(__file__).with_name("libsdq.so")
 BOOL, UINT8, UINT16, UINT32, UINT64 = 0, 1, 2, 3, 4
 INT8, INT16, INT32, INT64 = 5, 6, 7, 8
 FLOAT16, FLOAT32, FLOAT64, BFLOAT16, COMPLEX64 = 9, 10, 11, 12, 13
+
+# sdq_activation (include/sdq.h): the matmul epilogue's activation.
+ACT_NONE, ACT_GELU_APPROX = 0, 1
 
 _NP_OF = {
     FLOAT32: np.float32,
@@ -154,6 +159,10 @@ def _declare(L: ctypes.CDLL) -> None:
             c_int,
             [P(A), A, A, A, A, c_bool, COptionalInt, COptionalInt, ctypes.c_char_p, S],
         ),
+        "sdq_quantized_linear": (
+            c_int,
+            [P(A), A, A, A, A, A, c_int, COptionalInt, COptionalInt, ctypes.c_char_p, S],
+        ),
         "sdq_add": (c_int, [P(A), A, A, S]),
         "sdq_multiply": (c_int, [P(A), A, A, S]),
         "sdq_astype": (c_int, [P(A), A, c_int, S]),
@@ -164,6 +173,11 @@ def _declare(L: ctypes.CDLL) -> None:
             c_int,
             [c_vp, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
              ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp],
+        ),
+        "sdq_quantized_matmul_epilogue_raw": (
+            c_int,
+            [c_vp, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
+             ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
         ),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
         "sdq_array_device_ptr": (c_vp, [A]),
@@ -501,6 +515,24 @@ class QuantizedArray:
                                        _some_int(self.group_size), _some_int(self.bits),
                                        self.QUANT_MODE, stream._raw),
             "quantized_matmul",
+        )
+        return Array(res)
+
+    def linear(self, x: Array, stream: Stream, bias: Array | None = None,
+               activation: int = 0) -> Array:
+        """act(x @ weight.T + bias) in one launch: quantized::linear's
+        quantized branch with its bias add (quantized.rs:293-318) and an
+        optional activation (ACT_GELU_APPROX, the Flux MLP's GELU,
+        flux.rs:400-413), applied to the f32 accumulator before the output's
+        one rounding."""
+        res = CArray(None)
+        _check(
+            lib().sdq_quantized_linear(ctypes.byref(res), x._raw, self.weight._raw,
+                                       self.scales._raw, self.biases._raw,
+                                       bias._raw if bias is not None else CArray(None),
+                                       int(activation), _some_int(self.group_size),
+                                       _some_int(self.bits), self.QUANT_MODE, stream._raw),
+            "quantized_linear",
         )
         return Array(res)
 

@@ -208,3 +208,84 @@ def _sampled_check(oracle, sdq, stream, M, N, K, bits, seed, rows=48):
 ])
 def test_baseline_shapes(oracle, sdq, stream, M, N, K, bits):
     _sampled_check(oracle, sdq, stream, M, N, K, bits, seed=1000 + M + N + K)
+
+
+# ---- fused epilogue: act(x @ dequantize(w).T + bias) -----------------------------------
+
+
+def _gelu64(v):
+    c = np.float64(np.float32(0.7978845238685608))
+    return 0.5 * v * (1.0 + np.tanh((v + 0.044715 * v ** 3) * c))
+
+
+@pytest.mark.parametrize("M,N,K,bits", [
+    (1, 200, 512, 4),       # small-M kernel, direct store
+    (16, 64, 8192, 8),      # small-M kernel, split K (last-arriver store)
+    (100, 300, 256, 4),     # tile kernel, whole tiles
+    (300, 512, 8192, 4),    # tile kernel, split K (the reduction kernel stores)
+])
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("bias_dtype", ["f32", "bf16", None])
+def test_linear_epilogue_matches_the_composition(oracle, sdq, stream, M, N, K, bits, act, bias_dtype):
+    # quantized.rs:314-317 (bias after the matmul) and flux.rs:400-413 (GELU
+    # after the MLP's first linear), fused into the matmul's store.
+    print(f"linear M={M} N={N} K={K} bits={bits} act={act} bias={bias_dtype}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 1100 + N + bits, N, K, bits)
+    x_dev, x_vals = _x(oracle, sdq, 1101 + M, (M, K), "bf16")
+    b = oracle.normals(1102 + N, N)
+    bias = None
+    if bias_dtype == "f32":
+        bias = sdq.Array.from_numpy(b)
+    elif bias_dtype == "bf16":
+        bits16 = sdq.f32_to_bf16_bits(b)
+        bias, b = sdq.Array.from_numpy(bits16, sdq.BFLOAT16), sdq.bf16_bits_to_f32(bits16)
+    y = q.linear(x_dev, stream, bias=bias, activation=act)
+    assert y.dtype == sdq.FLOAT32 and y.shape == [M, N]
+    got = y.to_numpy()
+    v = x_vals.astype(np.float64) @ deq.astype(np.float64).T + (b if bias is not None else 0.0)
+    want = _gelu64(v) if act else v
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
+    # With f32 output the fused sum equals the unfused sequence exactly, and
+    # the GELU equals the elementwise op on it to its own bound.
+    plain = q.matmul(x_dev, stream).to_numpy()
+    pre = (plain + b.astype(np.float32)).astype(np.float32) if bias is not None else plain
+    if act:
+        assert np.max(np.abs(got - oracle.gelu_approx(pre))) <= 2e-6 + 1e-6 * np.max(np.abs(pre))
+    else:
+        assert np.array_equal(got, pre)
+
+
+def test_linear_epilogue_bf16_output_and_raw_entry(oracle, sdq, stream):
+    # bf16 scales give bf16 output: the epilogue works on the f32 accumulator
+    # and rounds once; the raw entry point computes the same bits.
+    import ctypes
+    M, N, K = 40, 96, 256
+    q, deq = _qweight(oracle, sdq, stream, 1200, N, K, 4, sdt="bf16")
+    x_dev, x_vals = _x(oracle, sdq, 1201, (M, K), "bf16")
+    b = oracle.normals(1202, N)
+    bias = sdq.Array.from_numpy(b)
+    y = q.linear(x_dev, stream, bias=bias, activation=sdq.ACT_GELU_APPROX)
+    assert y.dtype == sdq.BFLOAT16
+    got = sdq.bf16_bits_to_f32(y.to_numpy()).reshape(M, N)
+    want = _gelu64(x_vals.astype(np.float64) @ deq.astype(np.float64).T + b)
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
+    out = sdq.Array.from_numpy(np.zeros((M, N), np.uint16), sdq.BFLOAT16)
+    L = sdq.lib()
+    rc = L.sdq_quantized_matmul_epilogue_raw(
+        out.device_ptr, sdq.BFLOAT16, x_dev.device_ptr, sdq.BFLOAT16, K, q.weight.device_ptr,
+        q.scales.device_ptr, q.biases.device_ptr, sdq.BFLOAT16, M, N, K, 64, 4,
+        bias.device_ptr, sdq.FLOAT32, sdq.ACT_GELU_APPROX, stream.native)
+    assert rc == 0
+    stream.synchronize()
+    assert np.array_equal(out.to_numpy(), y.to_numpy())
+
+
+def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
+    q, _ = _qweight(oracle, sdq, stream, 1300, 64, 128, 4)
+    x_dev, _ = _x(oracle, sdq, 1301, (4, 128), "bf16")
+    with pytest.raises(sdq.Error, match="bias must be"):
+        q.linear(x_dev, stream, bias=sdq.Array.from_numpy(np.zeros(63, np.float32)))
+    with pytest.raises(sdq.Error, match="activation"):
+        q.linear(x_dev, stream, activation=7)
