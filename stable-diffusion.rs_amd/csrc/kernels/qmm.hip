@@ -451,14 +451,24 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   }
 
   // The epilogue needs only the column's bias: one value per lane per 32-row
-  // block of weights.
+  // block of weights.  The activation is chosen once for the whole tile: a
+  // per-element branch would end each element's LDS write in a wait.
   float bcol[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
-  store_tile([&](int mb, int j, float (&v)[16]) {
+  auto finish = [&](auto act) {
+    store_tile([&](int mb, int j, float (&v)[16]) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) v[e] = epi_apply(ep, acc[mb][j][e], bcol[j]);
-  });
+      for (int e = 0; e < 16; ++e) {
+        const float t = acc[mb][j][e] + bcol[j];
+        v[e] = decltype(act)::value ? gelu_approx_f(t) : t;
+      }
+    });
+  };
+  if (ep.act == 1)
+    finish(std::integral_constant<bool, true>{});
+  else
+    finish(std::integral_constant<bool, false>{});
 }
 
 // Sum of the K ranges of the split tiles, in range order (so the result does
