@@ -225,6 +225,32 @@ int sdq_quantized_linear(sdq_array *res, sdq_array x, sdq_array w,
                          int activation, sdq_optional_int group_size,
                          sdq_optional_int bits, const char *mode, sdq_stream s);
 
+/* How sdq_quantized_linear_combine merges the linear's output v with a
+ * second [..., N] operand r (and an optional per-column gate g). */
+typedef enum sdq_combine_ {
+  SDQ_COMBINE_NONE = 0,
+  SDQ_COMBINE_GATED_RESIDUAL = 1, /* y = r + g * v: Flux's x + gate * attn/mlp
+                                   * (flux.rs:389-398, 414, 470); g = 1 if absent */
+  SDQ_COMBINE_PRODUCT = 2,        /* y = v * r: T5's gelu(wi_0 x) * (wi_1 x)
+                                   * (t5.rs:209-214), v being the wi_0 linear
+                                   * with SDQ_ACT_GELU_APPROX */
+} sdq_combine;
+
+/* sdq_quantized_linear followed by the combine stage above:
+ * it replaces the mlx_multiply / mlx_add calls the reference issues after the
+ * linear at those call sites.  residual: the output's shape, any float
+ * dtype; gate: N values or a NULL-ctx handle.  For M <= 32 the whole
+ * epilogue runs in the matmul's store, on the f32 value; for larger M the
+ * combine stage runs as one in-place pass over the output right after the
+ * matmul, on v rounded to the output dtype (as the unfused sequence does). */
+int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w,
+                                 sdq_array scales, sdq_array biases,
+                                 sdq_array bias, int activation,
+                                 sdq_array residual, sdq_array gate,
+                                 int combine, sdq_optional_int group_size,
+                                 sdq_optional_int bits, const char *mode,
+                                 sdq_stream s);
+
 /* ---- elementwise ops the linear and its callers use ------------------------- */
 
 /* replaces mlx_add (mlx.rs:124) for the shapes the quantized linear needs:

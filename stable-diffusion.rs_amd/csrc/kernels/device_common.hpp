@@ -206,18 +206,31 @@ __device__ __forceinline__ float gelu_approx_f(float v) {
   return u >= 0.0f ? v * (1.0f - r) : v * r;
 }
 
+// One value of a float32/bfloat16/float16 array as f32.
+__device__ __forceinline__ float epi_load(const void *p, int dtype, int64_t i) {
+  if (dtype == SDQ_FLOAT32) return static_cast<const float *>(p)[i];
+  const uint16_t h = static_cast<const uint16_t *>(p)[i];
+  return dtype == SDQ_BFLOAT16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
 // The matmul epilogue (kern::Epilogue) on one f32 result: bias of output
 // column n, then the activation; the caller rounds once to the output dtype.
 __device__ __forceinline__ float epi_bias(const kern::Epilogue &ep, int64_t n) {
-  if (!ep.bias) return 0.0f;
-  if (ep.bias_dtype == SDQ_FLOAT32) return static_cast<const float *>(ep.bias)[n];
-  const uint16_t h = static_cast<const uint16_t *>(ep.bias)[n];
-  return ep.bias_dtype == SDQ_BFLOAT16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+  return ep.bias ? epi_load(ep.bias, ep.bias_dtype, n) : 0.0f;
 }
 
 __device__ __forceinline__ float epi_apply(const kern::Epilogue &ep, float v, float bias) {
   v += bias;
   return ep.act == 1 ? gelu_approx_f(v) : v;
+}
+
+// The combine stage of the epilogue for output element (m, n).
+__device__ __forceinline__ float epi_combine(const kern::Epilogue &ep, float v, int64_t m, int64_t n) {
+  if (ep.combine == 0) return v;
+  const float r = epi_load(ep.res, ep.res_dtype, m * ep.ld_res + n);
+  if (ep.combine == 2) return v * r;
+  const float g = ep.gate ? epi_load(ep.gate, ep.gate_dtype, n) : 1.0f;
+  return fmaf(g, v, r);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {

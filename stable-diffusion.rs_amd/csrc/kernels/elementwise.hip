@@ -87,6 +87,20 @@ __global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::
     out[i] = Elem<D>::store(gelu_approx_f(Elem<D>::load(a[i])));
 }
 
+// The epilogue's combine stage over a finished [M, N] output, in place:
+// y[m, n] = combine(y[m, n]) as in epi_combine.  Used after the large-M
+// kernel, whose tile store does not carry the combine stage.
+template <int D>
+__global__ __launch_bounds__(kThreads) void combine_kernel(typename Elem<D>::T *__restrict__ y,
+                                                           int64_t M, int64_t N,
+                                                           kern::Epilogue ep) {
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < M * N; i += stride) {
+    const int64_t m = i / N, n = i - m * N;
+    y[i] = Elem<D>::store(epi_combine(ep, Elem<D>::load(y[i]), m, n));
+  }
+}
+
 #define SDQ_FLOAT_DISPATCH(dt, NAME, ...)                                    \
   switch (dt) {                                                              \
   case SDQ_FLOAT32: {                                                        \
@@ -163,6 +177,17 @@ void gelu_approx(const void *a, int dtype, void *out, int64_t n,
         static_cast<typename Elem<D>::T *>(out), n, vec);
   });
   hip_check(hipGetLastError(), "gelu launch");
+}
+
+void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue &ep,
+                     hipStream_t stream) {
+  if (M == 0 || N == 0 || ep.combine == 0) return;
+  if (!epilogue_ok(ep)) fail("combine: bad epilogue");
+  const int grid = grid_for(M * N / 4 + 1);
+  SDQ_FLOAT_DISPATCH(y_dtype, D, {
+    combine_kernel<D><<<grid, kThreads, 0, stream>>>(static_cast<typename Elem<D>::T *>(y), M, N, ep);
+  });
+  hip_check(hipGetLastError(), "combine launch");
 }
 
 } // namespace kern

@@ -24,21 +24,44 @@ void dequantize(const uint32_t *wq, const void *scales, const void *biases,
                 int bits, void *out, int out_dtype, hipStream_t stream);
 
 // Output epilogue of the matmul kernels, applied to each f32 result before
-// its one rounding to the output dtype: y = act(acc + bias[n]).  `bias` is a
-// device pointer to N values (null: none) of `bias_dtype` (float32, bfloat16
-// or float16); act 0 = none, 1 = tanh-GELU.  It composes the bias add after
-// the quantized matmul (quantized.rs:314-317) and the GELU after the Flux
-// MLP's first linear (flux.rs:400-413) into the matmul's store.
+// the output's rounding:
+//   v = act(acc + bias[n])                      (bias optional, act 0 or GELU)
+//   y = v                                        combine 0
+//   y = res[m, n] + gate[n] * v                  combine 1 (gate optional: 1)
+//   y = v * res[m, n]                            combine 2
+// `bias` and `gate` are device pointers to N values, `res` to an [M, N]
+// tensor with row stride `ld_res` elements; each of float32, bfloat16 or
+// float16.  It fuses the calls that follow a quantized linear in the models:
+// the bias add (quantized.rs:314-317), the Flux MLP's GELU (flux.rs:400-413),
+// the gated residual x + gate * y (flux.rs:389-398, 414, 470) and T5's
+// gelu(wi_0 x) * (wi_1 x) (t5.rs:209-214).  The small-M kernel applies the
+// combine stage to the f32 value in its store; after the large-M kernel it
+// runs as one in-place pass over the output (combine_inplace), on the
+// rounded v, as the unfused sequence does.
 struct Epilogue {
   const void *bias = nullptr;
   int bias_dtype = 0;
   int act = 0;
+  const void *res = nullptr;
+  int res_dtype = 0;
+  int64_t ld_res = 0;
+  const void *gate = nullptr;
+  int gate_dtype = 0;
+  int combine = 0;
 };
 
+inline bool epi_dtype_ok(int dt) {
+  return dt == SDQ_FLOAT32 || dt == SDQ_BFLOAT16 || dt == SDQ_FLOAT16;
+}
+
 inline bool epilogue_ok(const Epilogue &ep) {
-  const bool dt = ep.bias_dtype == SDQ_FLOAT32 || ep.bias_dtype == SDQ_BFLOAT16 ||
-                  ep.bias_dtype == SDQ_FLOAT16;
-  return (ep.bias == nullptr || dt) && (ep.act == 0 || ep.act == 1);
+  if (ep.bias && !epi_dtype_ok(ep.bias_dtype)) return false;
+  if (ep.act != 0 && ep.act != 1) return false;
+  if (ep.combine == 0) return true;
+  if (ep.combine != 1 && ep.combine != 2) return false;
+  if (!ep.res || !epi_dtype_ok(ep.res_dtype)) return false;
+  if (ep.gate && (ep.combine != 1 || !epi_dtype_ok(ep.gate_dtype))) return false;
+  return true;
 }
 
 // Workspace the matmul kernels use when they split K across blocks: partial
@@ -98,6 +121,10 @@ void multiply(const void *a, int a_dtype, const void *b, int b_dtype,
               void *out, int out_dtype, int64_t n, hipStream_t stream);
 void gelu_approx(const void *a, int dtype, void *out, int64_t n,
                  hipStream_t stream);
+// The epilogue's combine stage (residual / gate / product) over a finished
+// y [M, N] in place; nothing when ep.combine == 0.
+void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue &ep,
+                     hipStream_t stream);
 
 // y [M, N] = a [M, K] @ b [N, K].T, f32 accumulate; y in the promotion of
 // the two dtypes.  dense.hip.

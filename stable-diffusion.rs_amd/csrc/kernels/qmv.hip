@@ -349,7 +349,8 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
 #pragma unroll
     for (int i = 0; i < kAcc; ++i) {
       const int m = 8 * (i / 4) + 4 * h + (i % 4);
-      if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(epi_apply(ep, acc[i], bn));
+      if (m < M && n < N)
+        y[int64_t(m) * N + n] = Elem<ODT>::store(epi_combine(ep, epi_apply(ep, acc[i], bn), m, n));
     }
     return;
   }
@@ -396,7 +397,8 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(
 #pragma unroll
   for (int i = 0; i < kAcc; ++i) {
     const int m = 8 * (i / 4) + 4 * h + (i % 4);
-    if (m < M && n < N) y[int64_t(m) * N + n] = Elem<ODT>::store(epi_apply(ep, v[i], bn));
+    if (m < M && n < N)
+      y[int64_t(m) * N + n] = Elem<ODT>::store(epi_combine(ep, epi_apply(ep, v[i], bn), m, n));
   }
   if (lane == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

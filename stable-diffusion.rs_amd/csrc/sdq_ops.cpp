@@ -112,8 +112,15 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
       *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
       ws.partial = static_cast<float *>((*keep_alive)->ptr);
     }
+    // The tile kernel fuses bias and activation; the combine stage follows
+    // as one in-place pass (the tile store with it grows the kernel ~6x).
+    kern::Epilogue ep_mm = ep;
+    ep_mm.combine = 0;
+    ep_mm.res = nullptr;
+    ep_mm.gate = nullptr;
     kern::qmm(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ws, ep, stream);
+              plan, ws, ep_mm, stream);
+    kern::combine_inplace(y, y_dtype, M, N, ep, stream);
   }
 }
 
@@ -226,7 +233,8 @@ namespace {
 void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
                            sdq_array biases, bool transpose, sdq_optional_int group_size,
                            sdq_optional_int bits, const char *mode, sdq_stream s,
-                           sdq_array bias, int activation) {
+                           sdq_array bias, int activation, sdq_array residual = sdq_array{nullptr},
+                           sdq_array gate = sdq_array{nullptr}, int combine = SDQ_COMBINE_NONE) {
     StreamImpl *st = stream_of(s, "quantized_matmul");
     check_mode(mode, sdq_array{nullptr});
     const int gs = opt_or(group_size, 64);
@@ -278,8 +286,40 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
     if (activation != SDQ_ACT_NONE && activation != SDQ_ACT_GELU_APPROX)
       fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(activation));
     ep.act = activation;
+    ArrayImpl *ra = nullptr, *ga = nullptr;
+    if (combine != SDQ_COMBINE_NONE) {
+      if (combine != SDQ_COMBINE_GATED_RESIDUAL && combine != SDQ_COMBINE_PRODUCT)
+        fail("combine must be SDQ_COMBINE_NONE, SDQ_COMBINE_GATED_RESIDUAL or SDQ_COMBINE_PRODUCT, got " +
+             std::to_string(combine));
+      if (!residual.ctx) fail("combine needs the residual (or product) operand");
+      ra = array_of(residual, "quantized_linear", "residual");
+      same_device(ra, st, "residual");
+      std::vector<int> want = xa->shape;
+      want.back() = int(N);
+      if (!is_float_dtype(ra->dtype) || ra->shape != want)
+        fail("residual must be a float array of the output's shape " + shape_str(want) + ", got " +
+             shape_str(ra->shape) + " " + dtype_name(ra->dtype));
+      ep.res = ra->data();
+      ep.res_dtype = ra->dtype;
+      ep.ld_res = N;
+      if (gate.ctx) {
+        if (combine != SDQ_COMBINE_GATED_RESIDUAL) fail("a gate applies to SDQ_COMBINE_GATED_RESIDUAL only");
+        ga = array_of(gate, "quantized_linear", "gate");
+        same_device(ga, st, "gate");
+        if (!is_float_dtype(ga->dtype) || ga->size != size_t(N) || (!ga->shape.empty() && ga->shape.back() != N))
+          fail("gate must be a float array of N = " + std::to_string(N) + " values, got " +
+               shape_str(ga->shape) + " " + dtype_name(ga->dtype));
+        ep.gate = ga->data();
+        ep.gate_dtype = ga->dtype;
+      }
+    } else if (residual.ctx || gate.ctx) {
+      fail("a residual or gate was given without a combine mode");
+    }
+    ep.combine = combine;
     const int out_dtype = promote_float(xa->dtype, sa->dtype);
     if (bb) order_after(bb, st);
+    if (ra) order_after(ra, st);
+    if (ga) order_after(ga, st);
     order_after(xa, st);
     order_after(wa, st);
     order_after(sa, st);
@@ -315,6 +355,17 @@ int sdq_quantized_linear(sdq_array *res, sdq_array x, sdq_array w, sdq_array sca
   SDQ_GUARD("quantized_linear", {
     quantized_matmul_impl(res, x, w, scales, biases, true, group_size, bits, mode, s, bias,
                           activation);
+  });
+}
+
+int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                                 sdq_array biases, sdq_array bias, int activation,
+                                 sdq_array residual, sdq_array gate, int combine,
+                                 sdq_optional_int group_size, sdq_optional_int bits,
+                                 const char *mode, sdq_stream s) {
+  SDQ_GUARD("quantized_linear_combine", {
+    quantized_matmul_impl(res, x, w, scales, biases, true, group_size, bits, mode, s, bias,
+                          activation, residual, gate, combine);
   });
 }
 
@@ -361,6 +412,7 @@ int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x, int x
     ep.bias = bias;
     ep.bias_dtype = bias ? bias_dtype : 0;
     ep.act = activation;
+    if (!kern::epilogue_ok(ep)) fail("bad epilogue");
     std::shared_ptr<Buffer> scratch;
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
                     group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch, ep);

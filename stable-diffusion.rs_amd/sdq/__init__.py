@@ -40,6 +40,9 @@ __all__ = [
     "UINT32",
     "ACT_NONE",
     "ACT_GELU_APPROX",
+    "COMBINE_NONE",
+    "COMBINE_GATED_RESIDUAL",
+    "COMBINE_PRODUCT",
     "f32_to_bf16_bits",
     "bf16_bits_to_f32",
 ]
@@ -51,8 +54,9 @@ BOOL, UINT8, UINT16, UINT32, UINT64 = 0, 1, 2, 3, 4
 INT8, INT16, INT32, INT64 = 5, 6, 7, 8
 FLOAT16, FLOAT32, FLOAT64, BFLOAT16, COMPLEX64 = 9, 10, 11, 12, 13
 
-# sdq_activation (include/sdq.h): the matmul epilogue's activation.
+# sdq_activation and sdq_combine (include/sdq.h): the matmul epilogue.
 ACT_NONE, ACT_GELU_APPROX = 0, 1
+COMBINE_NONE, COMBINE_GATED_RESIDUAL, COMBINE_PRODUCT = 0, 1, 2
 
 _NP_OF = {
     FLOAT32: np.float32,
@@ -162,6 +166,10 @@ def _declare(L: ctypes.CDLL) -> None:
         "sdq_quantized_linear": (
             c_int,
             [P(A), A, A, A, A, A, c_int, COptionalInt, COptionalInt, ctypes.c_char_p, S],
+        ),
+        "sdq_quantized_linear_combine": (
+            c_int,
+            [P(A), A, A, A, A, A, c_int, A, A, c_int, COptionalInt, COptionalInt, ctypes.c_char_p, S],
         ),
         "sdq_add": (c_int, [P(A), A, A, S]),
         "sdq_multiply": (c_int, [P(A), A, A, S]),
@@ -533,6 +541,23 @@ class QuantizedArray:
                                        int(activation), _some_int(self.group_size),
                                        _some_int(self.bits), self.QUANT_MODE, stream._raw),
             "quantized_linear",
+        )
+        return Array(res)
+
+    def linear_combine(self, x: Array, stream: Stream, residual: Array, combine: int,
+                       bias: Array | None = None, activation: int = 0,
+                       gate: Array | None = None) -> Array:
+        """`linear` followed by COMBINE_GATED_RESIDUAL (residual + gate * y,
+        Flux's gated residual, flux.rs:389-398) or COMBINE_PRODUCT (y *
+        residual, T5's gelu(wi_0 x) * (wi_1 x), t5.rs:209-214), one launch."""
+        res = CArray(None)
+        _check(
+            lib().sdq_quantized_linear_combine(
+                ctypes.byref(res), x._raw, self.weight._raw, self.scales._raw, self.biases._raw,
+                bias._raw if bias is not None else CArray(None), int(activation), residual._raw,
+                gate._raw if gate is not None else CArray(None), int(combine),
+                _some_int(self.group_size), _some_int(self.bits), self.QUANT_MODE, stream._raw),
+            "quantized_linear_combine",
         )
         return Array(res)
 

@@ -289,3 +289,57 @@ def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
         q.linear(x_dev, stream, bias=sdq.Array.from_numpy(np.zeros(63, np.float32)))
     with pytest.raises(sdq.Error, match="activation"):
         q.linear(x_dev, stream, activation=7)
+
+
+@pytest.mark.parametrize("M,N,K,bits", [
+    (1, 200, 512, 4),       # small-M kernel: combine in the store
+    (16, 64, 8192, 8),      # small-M kernel, split K
+    (100, 300, 256, 4),     # tile kernel, then the in-place combine pass
+    (300, 512, 8192, 4),    # tile kernel with split K and the reduction kernel
+])
+@pytest.mark.parametrize("mode", ["gated", "residual", "product"])
+def test_linear_combine_matches_the_composition(oracle, sdq, stream, M, N, K, bits, mode):
+    # Flux's gated residual x + gate * linear(h) (flux.rs:389-398) and T5's
+    # gelu(wi_0 x) * (wi_1 x) (t5.rs:209-214), as one call.
+    print(f"combine M={M} N={N} K={K} bits={bits} mode={mode}", flush=True)
+    q, deq = _qweight(oracle, sdq, stream, 1400 + N + bits, N, K, bits)
+    x_dev, x_vals = _x(oracle, sdq, 1401 + M, (M, K), "bf16")
+    b = oracle.normals(1402 + N, N)
+    r = oracle.normals(1403 + M, M * N).reshape(M, N)
+    g = oracle.normals(1404 + N, N, 0.5)
+    bits16 = sdq.f32_to_bf16_bits(r)
+    res, r = sdq.Array.from_numpy(bits16, sdq.BFLOAT16), sdq.bf16_bits_to_f32(bits16).reshape(M, N)
+    v = x_vals.astype(np.float64) @ deq.astype(np.float64).T + b
+    if mode == "product":
+        y = q.linear_combine(x_dev, stream, res, sdq.COMBINE_PRODUCT, bias=sdq.Array.from_numpy(b),
+                             activation=sdq.ACT_GELU_APPROX)
+        want = _gelu64(v) * r
+    elif mode == "gated":
+        y = q.linear_combine(x_dev, stream, res, sdq.COMBINE_GATED_RESIDUAL, bias=sdq.Array.from_numpy(b),
+                             gate=sdq.Array.from_numpy(g))
+        want = r + g * v
+    else:
+        y = q.linear_combine(x_dev, stream, res, sdq.COMBINE_GATED_RESIDUAL, bias=sdq.Array.from_numpy(b))
+        want = r + v
+    assert y.dtype == sdq.FLOAT32 and y.shape == [M, N]
+    got = y.to_numpy()
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
+    # Repeated calls agree bit for bit.
+    if mode == "gated":
+        again = q.linear_combine(x_dev, stream, res, sdq.COMBINE_GATED_RESIDUAL, bias=sdq.Array.from_numpy(b),
+                                 gate=sdq.Array.from_numpy(g)).to_numpy()
+        assert np.array_equal(again, got)
+
+
+def test_linear_combine_rejects_bad_arguments(oracle, sdq, stream):
+    q, _ = _qweight(oracle, sdq, stream, 1500, 64, 128, 4)
+    x_dev, _ = _x(oracle, sdq, 1501, (4, 128), "bf16")
+    good = sdq.Array.from_numpy(np.zeros((4, 64), np.float32))
+    with pytest.raises(sdq.Error, match="residual must be"):
+        q.linear_combine(x_dev, stream, sdq.Array.from_numpy(np.zeros((4, 63), np.float32)),
+                         sdq.COMBINE_GATED_RESIDUAL)
+    with pytest.raises(sdq.Error, match="gate applies"):
+        q.linear_combine(x_dev, stream, good, sdq.COMBINE_PRODUCT, gate=sdq.Array.from_numpy(np.ones(64, np.float32)))
+    with pytest.raises(sdq.Error, match="combine must be"):
+        q.linear_combine(x_dev, stream, good, 9)
