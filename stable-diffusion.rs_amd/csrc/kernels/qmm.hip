@@ -433,20 +433,22 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   };
 
   if (bid >= wk.dp_tiles) {
-    // A K range of a split tile: its f32 accumulators go to the workspace
-    // register-major (entry ((mb*2 + j)*16 + e) of thread t at float
-    // ((mb*2 + j)*16 + e)*256 + t of the range's slot), so that each store
-    // instruction writes 256 consecutive bytes per wave; rows past M are
-    // written too and never read.  The reduction kernel that follows on the
-    // stream adds the ranges in order.
+    // A K range of a split tile: its f32 accumulators go to the workspace in
+    // 16-byte pieces, register-major: entries 4q..4q+3 of MFMA tile (mb, j)
+    // of thread t at float4 ((mb*2 + j)*4 + q)*256 + t of the range's slot,
+    // so each store instruction writes 1 KB contiguous per wave.  Rows past M
+    // are written too and never read.  The reduction kernel that follows on
+    // the stream adds the ranges in order.
     const int64_t slot = int64_t(tile - wk.dp_tiles) * wk.splits + split;
-    float *mine = wk.partial + slot * (BM * kTileN) + tid;
+    float4 *mine = reinterpret_cast<float4 *>(wk.partial + slot * (BM * kTileN)) + tid;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mine[((mb * 2 + j) * 16 + e) * kThreads] = acc[mb][j][e];
+        for (int q = 0; q < 4; ++q)
+          mine[((mb * 2 + j) * 4 + q) * kThreads] =
+              float4{acc[mb][j][4 * q], acc[mb][j][4 * q + 1], acc[mb][j][4 * q + 2], acc[mb][j][4 * q + 3]};
     return;
   }
 
@@ -472,26 +474,25 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
 }
 
 // Sum of the K ranges of the split tiles, in range order (so the result does
-// not depend on which block finished first), converted to the output type.
-// Thread t of the launch handles four consecutive floats of the
-// register-major partial layout: threads 4c..4c+3 of one MFMA tile entry,
-// i.e. four consecutive columns of one output row.
+// not depend on which block finished first), with the epilogue, converted to
+// the output type.  Thread i of the launch takes float4 i of the partial
+// layout: four consecutive rows of one column (accumulator entries 4q..4q+3
+// of one MFMA tile of one tile-kernel thread).
 template <int ODT>
 __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
                                                          const float *__restrict__ partial,
                                                          int M, int N, int bm, int tiles_n,
                                                          int dp_tiles, int splits,
                                                          kern::Epilogue ep) {
-  using OT = typename Elem<ODT>::T;
   const int per_tile = bm * (kTileN / 4); // float4 pieces of one partial tile
   const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int sk = int(idx / per_tile);
   const int within = int(idx % per_tile);
-  const int reg = within / (kThreads / 4);       // (mb*2 + j)*16 + e
-  const int t = 4 * (within % (kThreads / 4));  // first of four threads
+  const int reg4 = within / kThreads;      // (mb*2 + j)*4 + q
+  const int t = within % kThreads;         // the tile kernel's thread
   const int lane = t & 63, wave = t >> 6;
-  const int mb = reg >> 5, j = (reg >> 4) & 1, e = reg & 15;
-  const int row = 32 * mb + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+  const int mb = reg4 >> 3, j = (reg4 >> 2) & 1, q = reg4 & 3;
+  const int row = 32 * mb + 8 * q + 4 * (lane >> 5);  // first of four rows
   const int col = wave * 64 + 32 * j + (lane & 31);
   const int tile = dp_tiles + sk;
   const int grow = (tile / tiles_n) * bm + row;
@@ -502,35 +503,22 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
   for (int p0 = 1; p0 < splits; p0 += 4) {
     float4 v[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (p0 + q < splits) v[q] = src[int64_t(p0 + q) * per_tile];
+    for (int u = 0; u < 4; ++u)
+      if (p0 + u < splits) v[u] = src[int64_t(p0 + u) * per_tile];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (p0 + q < splits) {
-        sum.x += v[q].x;
-        sum.y += v[q].y;
-        sum.z += v[q].z;
-        sum.w += v[q].w;
+    for (int u = 0; u < 4; ++u)
+      if (p0 + u < splits) {
+        sum.x += v[u].x;
+        sum.y += v[u].y;
+        sum.z += v[u].z;
+        sum.w += v[u].w;
       }
   }
-  OT *d = y + int64_t(grow) * N + gcol;
-  float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+  const float b = epi_bias(ep, gcol);
+  const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
-  for (int q = 0; q < 4; ++q) s4[q] = epi_apply(ep, s4[q], epi_bias(ep, min(gcol + q, N - 1)));
-  if (gcol + 4 <= N && (reinterpret_cast<uintptr_t>(d) % (4 * sizeof(OT))) == 0) {
-    if constexpr (sizeof(OT) == 4) {
-      *reinterpret_cast<float4 *>(d) = float4{s4[0], s4[1], s4[2], s4[3]};
-    } else {
-      uint2 v;
-      v.x = uint32_t(Elem<ODT>::store(s4[0])) | (uint32_t(Elem<ODT>::store(s4[1])) << 16);
-      v.y = uint32_t(Elem<ODT>::store(s4[2])) | (uint32_t(Elem<ODT>::store(s4[3])) << 16);
-      *reinterpret_cast<uint2 *>(d) = v;
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (gcol + q < N) d[q] = Elem<ODT>::store(s4[q]);
-  }
+  for (int u = 0; u < 4; ++u)
+    if (grow + u < M) y[int64_t(grow + u) * N + gcol] = Elem<ODT>::store(epi_apply(ep, s4[u], b));
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int BM>
