@@ -343,3 +343,41 @@ def test_linear_combine_rejects_bad_arguments(oracle, sdq, stream):
         q.linear_combine(x_dev, stream, good, sdq.COMBINE_PRODUCT, gate=sdq.Array.from_numpy(np.ones(64, np.float32)))
     with pytest.raises(sdq.Error, match="combine must be"):
         q.linear_combine(x_dev, stream, good, 9)
+
+
+@pytest.mark.parametrize("M", [3, 80])
+def test_linear_epilogue_f16_activations_and_scales(oracle, sdq, stream, M):
+    # f16 x with f16 scales give f16 output; bias in f16; GELU epilogue.
+    N, K = 160, 256
+    w = oracle.normals(1600 + M, N * K, 0.02).reshape(N, K)
+    wh = w.astype(np.float16)
+    q = sdq.QuantizedArray.quantize(sdq.Array.from_numpy(wh), 64, 4, stream)
+    wq, s, b = oracle.quantize(wh.astype(np.float32), 64, 4, 9)
+    deq = oracle.dequantize(wq, s, b, 64, 4, 9)
+    x = oracle.normals(1601 + M, M * K).reshape(M, K).astype(np.float16)
+    bias = oracle.normals(1602, N).astype(np.float16)
+    y = q.linear(sdq.Array.from_numpy(x), stream, bias=sdq.Array.from_numpy(bias),
+                 activation=sdq.ACT_GELU_APPROX)
+    assert y.dtype == sdq.FLOAT16 and y.shape == [M, N]
+    got = y.to_numpy().astype(np.float32)
+    want = _gelu64(x.astype(np.float64) @ deq.astype(np.float64).T + bias.astype(np.float64))
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
+
+
+@pytest.mark.parametrize("M", [12, 300])
+def test_linear_combine_on_flux_token_layout(oracle, sdq, stream, M):
+    # Flux feeds [1, seq, K] tokens and adds the gated output to a [1, seq, N]
+    # residual stream (flux.rs:389-398).
+    N, K = 256, 512
+    q, deq = _qweight(oracle, sdq, stream, 1700 + M, N, K, 4)
+    x_dev, x_vals = _x(oracle, sdq, 1701 + M, (1, M, K), "bf16")
+    r = oracle.normals(1702 + M, M * N).reshape(1, M, N)
+    g = oracle.normals(1703, N, 0.3)
+    y = q.linear_combine(x_dev, stream, sdq.Array.from_numpy(r), sdq.COMBINE_GATED_RESIDUAL,
+                         gate=sdq.Array.from_numpy(g))
+    assert y.shape == [1, M, N]
+    want = r[0] + g * (x_vals[0].astype(np.float64) @ deq.astype(np.float64).T)
+    got = y.to_numpy().reshape(M, N)
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= MAX_REL and cos >= MIN_COS, (err, cos)
