@@ -89,13 +89,48 @@ __global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::
 
 // The epilogue's combine stage over a finished [M, N] output, in place:
 // y[m, n] = combine(y[m, n]) as in epi_combine.  Used after the large-M
-// kernel, whose tile store does not carry the combine stage.
+// kernel, whose tile store does not carry the combine stage.  Groups of
+// eight consecutive elements of a row per thread (16-byte accesses) where
+// rows are whole groups and y is aligned (`vec`), else one element.
 template <int D>
 __global__ __launch_bounds__(kThreads) void combine_kernel(typename Elem<D>::T *__restrict__ y,
                                                            int64_t M, int64_t N,
-                                                           kern::Epilogue ep) {
+                                                           kern::Epilogue ep, bool vec) {
+  using T = typename Elem<D>::T;
+  constexpr int kWords = int(sizeof(T)) * 8 / 4; // 32-bit words per 8 elements
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < M * N; i += stride) {
+  const int64_t tid = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (vec) {
+    const int64_t groups = M * N / 8;
+    for (int64_t g = tid; g < groups; g += stride) {
+      const int64_t e0 = g * 8;
+      const int64_t m = e0 / N, n0 = e0 - m * N;
+      u32x4 *p = reinterpret_cast<u32x4 *>(y + e0);
+      u32x4 w[kWords / 4];
+#pragma unroll
+      for (int q = 0; q < kWords / 4; ++q) w[q] = p[q];
+#pragma unroll
+      for (int q = 0; q < kWords / 4; ++q) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t word = w[q][k];
+          if constexpr (sizeof(T) == 4) {
+            const int64_t n = n0 + 4 * q + k;
+            w[q][k] = __float_as_uint(epi_combine(ep, __uint_as_float(word), m, n));
+          } else {
+            const int64_t n = n0 + 8 * q + 2 * k;
+            const float lo = epi_combine(ep, Elem<D>::load(T(word & 0xffffu)), m, n);
+            const float hi = epi_combine(ep, Elem<D>::load(T(word >> 16)), m, n + 1);
+            w[q][k] = uint32_t(Elem<D>::store(lo)) | (uint32_t(Elem<D>::store(hi)) << 16);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kWords / 4; ++q) p[q] = w[q];
+    }
+    return;
+  }
+  for (int64_t i = tid; i < M * N; i += stride) {
     const int64_t m = i / N, n = i - m * N;
     y[i] = Elem<D>::store(epi_combine(ep, Elem<D>::load(y[i]), m, n));
   }
@@ -183,9 +218,11 @@ void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue 
                      hipStream_t stream) {
   if (M == 0 || N == 0 || ep.combine == 0) return;
   if (!epilogue_ok(ep)) fail("combine: bad epilogue");
-  const int grid = grid_for(M * N / 4 + 1);
+  const bool vec = N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  const int grid = grid_for((vec ? M * N / 8 : M * N) / 4 + 1);
   SDQ_FLOAT_DISPATCH(y_dtype, D, {
-    combine_kernel<D><<<grid, kThreads, 0, stream>>>(static_cast<typename Elem<D>::T *>(y), M, N, ep);
+    combine_kernel<D><<<grid, kThreads, 0, stream>>>(static_cast<typename Elem<D>::T *>(y), M, N, ep,
+                                                     vec);
   });
   hip_check(hipGetLastError(), "combine launch");
 }
