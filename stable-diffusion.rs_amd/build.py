@@ -38,16 +38,36 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-# Sources and their extra flags.  quant.hip must round every operation once
-# (bit-exact quantize/dequantize), so contraction into FMA is off there.
+# dtype codes (include/sdq.h) of the (activation, scales, output) combinations
+# the matmul kernels are instantiated for; qmm.hip / qmv.hip dispatch over the
+# same list, and a combination missing here is a link error.
+F16, F32, BF16 = 9, 10, 12
+MATMUL_COMBOS = [
+    (BF16, F32, F32), (BF16, BF16, BF16), (F32, F32, F32), (BF16, F32, BF16), (F16, F16, F16),
+    (F16, F32, F32), (F32, BF16, F32), (F32, F16, F32), (BF16, F16, F32), (F16, BF16, F32),
+]
+
+
+def _combo_flags(c):
+    return [f"-DSDQ_XD={c[0]}", f"-DSDQ_SD={c[1]}", f"-DSDQ_OD={c[2]}"]
+
+
+# Sources, their extra flags and object names.  quant.hip must round every
+# operation once (bit-exact quantize/dequantize), so contraction into FMA is
+# off there.  The matmul kernels' instantiation units are compiled once per
+# dtype combination.
 SOURCES = [
-    (CSRC / "sdq_runtime.cpp", []),
-    (CSRC / "sdq_ops.cpp", []),
-    (CSRC / "kernels" / "quant.hip", ["-ffp-contract=off"]),
-    (CSRC / "kernels" / "elementwise.hip", []),
-    (CSRC / "kernels" / "dense.hip", []),
-    (CSRC / "kernels" / "qmv.hip", []),
-    (CSRC / "kernels" / "qmm.hip", []),
+    (CSRC / "sdq_runtime.cpp", [], None),
+    (CSRC / "sdq_ops.cpp", [], None),
+    (CSRC / "kernels" / "quant.hip", ["-ffp-contract=off"], None),
+    (CSRC / "kernels" / "elementwise.hip", [], None),
+    (CSRC / "kernels" / "dense.hip", [], None),
+    (CSRC / "kernels" / "qmv.hip", [], None),
+    (CSRC / "kernels" / "qmm.hip", [], None),
+] + [
+    (CSRC / "kernels" / f"{k}_inst.hip", _combo_flags(c), f"{k}_inst_{c[0]}_{c[1]}_{c[2]}")
+    for k in ("qmm", "qmv")
+    for c in MATMUL_COMBOS
 ]
 
 
@@ -67,8 +87,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(lines), flush=True)
 
 
-def _compile(src: Path, extra: list[str], verbose: bool) -> Path:
-    obj = BUILD / (src.stem + src.suffix.replace(".", "_") + ".o")
+def _compile(src: Path, extra: list[str], name: str | None, verbose: bool) -> Path:
+    obj = BUILD / ((name or src.stem + src.suffix.replace(".", "_")) + ".o")
     cmd = [HIPCC, *COMMON, *extra, "-c", str(src), "-o", str(obj)]
     _run(cmd, verbose)
     return obj
@@ -76,9 +96,11 @@ def _compile(src: Path, extra: list[str], verbose: bool) -> Path:
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     BUILD.mkdir(parents=True, exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 8)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
+    # Longest compiles first, so the pool's tail is short.
+    order = sorted(SOURCES, key=lambda s: 0 if s[0].name.startswith(("qmm", "qmv")) else 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, src, extra, verbose) for src, extra in SOURCES]
+        futs = [ex.submit(_compile, src, extra, name, verbose) for src, extra, name in order]
         objs = [f.result() for f in futs]
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)], verbose)

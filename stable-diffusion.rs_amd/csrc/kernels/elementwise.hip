@@ -200,6 +200,7 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(typename Elem<D>::T *
 
 namespace kern {
 
+
 void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,
             hipStream_t stream) {
   if (n == 0) return;

@@ -64,21 +64,22 @@ inline bool epilogue_ok(const Epilogue &ep) {
   return true;
 }
 
-// Workspace the matmul kernels use when they split K across blocks: partial
-// tiles, and for qmv one counter per split tile (zero on entry; the kernel
-// leaves them zero).  qmm adds its partials in a second kernel and needs no
-// counters.
+// Workspace the large-M kernel uses when it splits K across blocks: f32
+// partial tiles, added by a second kernel.
 struct SplitWorkspace {
   float *partial = nullptr;
-  unsigned *counters = nullptr;
 };
 
+// Launch plan of the small-M kernel: each block owns `tiles_per_block`
+// tiles of 16 weight rows and all of K; each tile is streamed by `waves`
+// waves over contiguous K ranges, whose partial tiles are added in LDS.
 struct QmvPlan {
-  int waves = 4;             // waves (32-row tiles) per block: 1 or 4
-  int splits = 1;            // K ranges
-  int groups_per_split = 0;  // 64-wide steps per range
-  size_t partial_floats = 0; // workspace needed (0 when splits == 1)
-  int counters = 0;          // 32-row tiles
+  int tiles_per_block = 1; // T
+  int waves = 4;           // S: K ranges per tile (the block has T * S waves)
+  int row_blocks = 1;      // 16-token MFMA row blocks: 1 for M <= 16, 2 for M <= 32
+  int xmode = 1;           // where x comes from: 0 read per chunk, 1 staged per
+                           // wave, 2 staged once per block
+  int lds_bytes = 0;       // dynamic LDS of one block
 };
 
 // y [M, N] = x [M, K] @ dequantize(w).T for M <= 32.  qmv.hip.
@@ -86,8 +87,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
 void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, const QmvPlan &plan, const SplitWorkspace &ws,
-         const Epilogue &ep, hipStream_t stream);
+         int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream);
 
 // Tile and split-K plan of one qmm launch (a pure function of the shape and
 // the CU count).

@@ -1,23 +1,9 @@
-// qmm.hip -- y = x @ dequantize(w).T for many rows of x: the prefill-shaped,
-// MFMA-bound side of mlx_quantized_matmul (crates/sd-tensor/src/mlx.rs:386-397,
-// 1947-1975; e.g. every Flux block linear at 4096+512 tokens,
-// sd-models/src/mlx/flux.rs:333-471).
-//
-// Block tile BM x 256, four waves.  Wave v owns output columns
-// [64v, 64v + 64) of the tile and all BM rows, i.e. BM/32 x 2 MFMA tiles of
-// 32 x 32 (v_mfma_f32_32x32x16_bf16, fp32 accumulate).  Per 64-wide K step:
-//   * the block stages the BM x 64 activation tile into LDS as bf16
-//     (double-buffered, 16-byte chunks XOR-swizzled by row so the MFMA
-//     operand reads are conflict-free); every wave reads all of it;
-//   * each wave loads only ITS weight rows -- 16 B (4-bit) or 32 B (8-bit)
-//     per lane per 32-row block -- and dequantizes them in registers,
-//     scale * q + bias in f32, straight into the bf16 B operand.  A weight
-//     element is dequantized once per block and used for BM rows, which is
-//     what keeps the unpack cost under the MFMA time.
-// Lane (r, h) = (lane % 32, lane / 32) feeds its eight K elements of k-step i
-// from k = 64*step + 32*h + 8*i + e for both operands.
+// qmm.hip -- the launch planner and dtype dispatch of the large-M tile kernel
+// (qmm_kernel.hpp holds the kernel; qmm_inst.hip instantiates it per dtype
+// combination): the MFMA-bound side of mlx_quantized_matmul
+// (crates/sd-tensor/src/mlx.rs:386-397, 1947-1975).
 #include <algorithm>
-#include <type_traits>
+#include <string>
 
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -25,557 +11,27 @@
 #include "../sdq_internal.hpp"
 
 namespace sdq {
-namespace {
+namespace qmm_detail {
 
-using namespace dev;
-
-constexpr int kThreads = 256;
 constexpr int kTileN = 256;
 
-__device__ __forceinline__ float byte_f(uint32_t v, int b) {
-  return float((v >> (8 * b)) & 0xffu);
-}
+// One activation/scale/output dtype combination of the tile kernel, for 4 or
+// 8 bits: instantiated once per combination in its own translation unit
+// (qmm_inst.hip, compiled once per combination) so the build runs in parallel.
+template <int XD, int SD, int OD>
+void qmm_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
+               const void *b, int M, int N, int K, int gs, const kern::QmmPlan &plan,
+               const kern::SplitWorkspace &ws, const kern::Epilogue &ep, hipStream_t st);
 
-// Eight dequantized weights of k-step i, in element order, as bf16.
-template <int BITS>
-__device__ __forceinline__ u32x4 dequant8(const u32x4 (&wr)[BITS / 4], int i, float s, float b);
+} // namespace qmm_detail
 
-template <>
-__device__ __forceinline__ u32x4 dequant8<4>(const u32x4 (&wr)[1], int i, float s, float b) {
-  const uint32_t wd = wr[0][i];
-  const uint32_t lo = opaque(wd & 0x0F0F0F0Fu);        // codes 0, 2, 4, 6
-  const uint32_t hi = opaque((wd >> 4) & 0x0F0F0F0Fu); // codes 1, 3, 5, 7
-  u32x4 r;
-#pragma unroll
-  for (int d = 0; d < 4; ++d)
-    r[d] = pack_bf16x2(fmaf(byte_f(lo, d), s, b), fmaf(byte_f(hi, d), s, b));
-  return r;
-}
-
-template <>
-__device__ __forceinline__ u32x4 dequant8<8>(const u32x4 (&wr)[2], int i, float s, float b) {
-  const uint32_t w0 = wr[i / 2][(i % 2) * 2];
-  const uint32_t w1 = wr[i / 2][(i % 2) * 2 + 1];
-  u32x4 r;
-  r[0] = pack_bf16x2(fmaf(byte_f(w0, 0), s, b), fmaf(byte_f(w0, 1), s, b));
-  r[1] = pack_bf16x2(fmaf(byte_f(w0, 2), s, b), fmaf(byte_f(w0, 3), s, b));
-  r[2] = pack_bf16x2(fmaf(byte_f(w1, 0), s, b), fmaf(byte_f(w1, 1), s, b));
-  r[3] = pack_bf16x2(fmaf(byte_f(w1, 2), s, b), fmaf(byte_f(w1, 3), s, b));
-  return r;
-}
-
-// Work assignment of one launch.  Tiles are numbered M-tile major; tiles
-// [0, dp_tiles) are computed whole, one block each; each tile after that is
-// split into `splits` K ranges of `steps_per_split` 64-wide steps, one block
-// per range, each writing its f32 partial tile to `partial`
-// ([split tile][range][BM][256], row-major); qmm_reduce_kernel adds them.
-struct QmmWork {
-  int tiles_n;
-  int dp_tiles;
-  int splits;
-  int steps_per_split;
-  float *partial;
-};
-
-template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH>
-__global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
-    typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
-    int64_t ldx, const uint32_t *__restrict__ w,
-    const typename Elem<SDT>::T *__restrict__ scales,
-    const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, QmmWork wk,
-    kern::Epilogue ep) {
-  using XT = typename Elem<XDT>::T;
-  using ST = typename Elem<SDT>::T;
-  constexpr int MB = BM / 32;           // 32-row MFMA blocks per wave
-  constexpr int kWordsPerStep = 2 * BITS; // 64 codes of one row
-  constexpr int kHalfWords = BITS;        // this lane half's share
-  constexpr int kWV = BITS / 4;           // u32x4 per lane per 32-row block
-  // Three stages of BM rows x 64 bf16 (128 B = 32 words per row).
-  constexpr int kStage = BM * 32;
-  __shared__ __attribute__((aligned(16))) uint32_t xs[3 * kStage];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int r = lane & 31;
-  const int h = lane >> 5;
-  const int steps = K / 64;
-  const int groups = K / GS;
-  const int bid = blockIdx.x;
-  int tile = bid, split = 0, k_begin = 0, k_end = steps;
-  if (bid >= wk.dp_tiles) {
-    const int j = bid - wk.dp_tiles;
-    tile = wk.dp_tiles + j / wk.splits;
-    split = j % wk.splits;
-    k_begin = split * wk.steps_per_split;
-    k_end = min(steps, k_begin + wk.steps_per_split);
-  }
-  const int m0 = (tile / wk.tiles_n) * BM;
-  const int nw = (tile % wk.tiles_n) * kTileN + wave * 64;
-  const int k_last = k_end - 1;
-
-  // Buffer windows (byte offsets fit in 32 bits: checked on the host).
-  const Rsrc rx = make_rsrc(x, uint32_t((int64_t(M - 1) * ldx + K) * sizeof(XT)));
-  const Rsrc rw = make_rsrc(w, uint32_t(int64_t(N) * K * BITS / 8));
-  const Rsrc rs = make_rsrc(scales, uint32_t(int64_t(N) * groups * sizeof(ST)));
-  const Rsrc rb = make_rsrc(biases, uint32_t(int64_t(N) * groups * sizeof(ST)));
-
-  uint32_t woff[2], soff[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = nw + 32 * j + r;
-    const int nrow = n < N ? n : N - 1; // rows past N are read, never stored
-    woff[j] = uint32_t((int64_t(nrow) * (int64_t(K) * BITS / 32) + h * kHalfWords) * 4);
-    soff[j] = uint32_t(int64_t(nrow) * groups * sizeof(ST));
-  }
-
-  // Staging: thread t moves 16-byte chunk (t % 8) of rows t/8 + 32q.  Rows
-  // past M re-read row M - 1 (their products are never stored), so every
-  // load is unconditional and each wait counts exactly the loads it needs.
-  const int sc = tid & 7;
-  const int sr = tid >> 3;
-  uint32_t xoff[MB];
-#pragma unroll
-  for (int q = 0; q < MB; ++q)
-    xoff[q] = uint32_t((int64_t(min(m0 + sr + 32 * q, M - 1)) * ldx + 8 * sc) * sizeof(XT));
-  auto stage_load = [&](int step, u32x4 (&xr)[MB]) {
-    const uint32_t so = uint32_t(step) * 64 * sizeof(XT);
-#pragma unroll
-    for (int q = 0; q < MB; ++q) xr[q] = BLoad8<XDT>::get(rx, xoff[q], so);
-  };
-  // Chunk c of row `row` sits at chunk c ^ ((row >> 1) & 7) of that row, so
-  // the MFMA operand reads below hit all 64 banks without conflicts.
-  auto stage_store = [&](uint32_t *dst, const u32x4 (&xr)[MB]) {
-#pragma unroll
-    for (int q = 0; q < MB; ++q) {
-      const int row = sr + 32 * q;
-      *reinterpret_cast<u32x4 *>(&dst[row * 32 + ((sc ^ ((row >> 1) & 7)) * 4)]) = xr[q];
-    }
-  };
-  // A fragment of 32-row block mb for k-step i.
-  auto read_a = [&](const uint32_t *src, int i, int mb) {
-    const int chunk = (4 * h + i) ^ ((r >> 1) & 7);
-    return *reinterpret_cast<const u32x4 *>(&src[(mb * 32 + r) * 32 + chunk * 4]);
-  };
-  struct WStep {
-    u32x4 q[2][kWV];
-    float s[2], b[2];
-  };
-  auto load_w = [&](int step, WStep &ws) {
-    const uint32_t wso = uint32_t(step) * kWordsPerStep * 4;
-    const uint32_t sso = uint32_t((step * 64) / GS) * sizeof(ST);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int v = 0; v < kWV; ++v) ws.q[j][v] = bload16(rw, woff[j] + 16 * v, wso);
-      ws.s[j] = BLoadScalar<SDT>::get(rs, soff[j], sso);
-      ws.b[j] = BLoadScalar<SDT>::get(rb, soff[j], sso);
-    }
-  };
-  auto dequant = [&](const WStep &ws, int i, u32x4 (&dst)[2]) {
-    dst[0] = dequant8<BITS>(ws.q[0], i, ws.s[0], ws.b[0]);
-    dst[1] = dequant8<BITS>(ws.q[1], i, ws.s[1], ws.b[1]);
-  };
-
-  // Scale and bias chunks (SCH): a 16-byte load brings kCG consecutive
-  // groups of one row, so each row's scales and biases cost one load per
-  // kCG groups instead of one per step -- a load instruction's cost is set
-  // by the distinct cache lines it touches (32 rows here), not its bytes.
-  // Needs 16-byte aligned scale rows; the host picks SCH accordingly.
-  constexpr int kCG = 16 / int(sizeof(ST));
-  auto chunk_of = [&](int step) { return ((step * 64) / GS) / kCG; };
-  auto load_chunk = [&](int c, u32x4 (&cs)[2], u32x4 (&cb)[2]) {
-    const uint32_t off = uint32_t(c) * 16;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      cs[j] = bload16(rs, soff[j], off);
-      cb[j] = bload16(rb, soff[j], off);
-    }
-  };
-  auto pick = [&](const u32x4 &v, int e) -> float {
-    if constexpr (sizeof(ST) == 4) {
-      const uint32_t wv = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
-      return __uint_as_float(wv);
-    } else {
-      const int d = e >> 1;
-      const uint32_t wv = d == 0 ? v[0] : d == 1 ? v[1] : d == 2 ? v[2] : v[3];
-      return Elem<SDT>::load(typename Elem<SDT>::T((e & 1) ? (wv >> 16) : (wv & 0xffffu)));
-    }
-  };
-
-  floatx16 acc[MB][2];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[mb][j][e] = 0.0f;
-
-  // Software pipeline, per 64-wide step s of this block's K range:
-  //   * weights: codes, scales and biases of step s + 2 are loaded at the top
-  //     of step s (a three-deep register queue);
-  //   * activations: the tile of step s + 2 arrives in registers during step
-  //     s - 1 and is written to LDS stage (s + 2) % 3 in the third k-step of
-  //     step s, when the tile of step s + 3 is requested; one barrier per
-  //     step makes it visible;
-  //   * operands: the A fragments and dequantized B fragments of k-step i + 1
-  //     are prepared while the MFMAs of k-step i run -- across the step
-  //     boundary too, since stage (s + 1) % 3 is complete before step s ends.
-  // Steps past the range re-read its last step, never used, so the body has
-  // no branches.
-  WStep w0, w1, w2;
-  u32x4 xr[MB];
-  stage_load(k_begin, xr);
-  stage_store(xs, xr);
-  stage_load(min(k_begin + 1, k_last), xr);
-  stage_store(xs + kStage, xr);
-  stage_load(min(k_begin + 2, k_last), xr);
-  load_w(k_begin, w0);
-  load_w(min(k_begin + 1, k_last), w1);
-  // SCH: one chunk in registers, always the one holding step s + 1 at the
-  // top of step s.  That step's scale and bias are picked from it there (the
-  // weight queue entry of step s + 1 was loaded without them), then the chunk
-  // of step s + 2 is loaded if it differs -- a full step before its first
-  // pick, and with no register copy that would wait for the load.
-  u32x4 cs[2], cb[2];
-  int c_cur = 0;
-  if constexpr (SCH) {
-    c_cur = chunk_of(min(k_begin + 1, k_last));
-    load_chunk(c_cur, cs, cb);
-  }
-  __syncthreads();
-
-  u32x4 a[MB];
-  u32x4 bq[2][2];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) a[mb] = read_a(xs, 0, mb);
-  dequant(w0, 0, bq[0]);
-
-  // Dequantization of one k-step for both 32-row blocks of weights, cut into
-  // pieces that are spread over the MFMA slots below (block j's pieces are
-  // numbered j * kPieces + piece).  4-bit: piece 0 splits the word into even
-  // and odd codes, pieces 1-4 each produce one packed bf16 pair.  8-bit:
-  // pieces 0-3 each produce one pair.
-  constexpr int kPieces = BITS == 4 ? 5 : 4;
-  constexpr int kSlots = 2 * MB;    // MFMAs per k-step
-  constexpr int kRefillLag = 4;     // slots between an A fragment's last MFMA and its refill
-  uint32_t lo[2], hi[2];
-  auto dq_piece = [&](const WStep &ws, int i, int j, int piece, u32x4 &dst) {
-    const float sc_ = ws.s[j], bi_ = ws.b[j];
-    if constexpr (BITS == 4) {
-      if (piece == 0) {
-        const uint32_t wd = ws.q[j][0][i];
-        lo[j] = opaque(wd & 0x0F0F0F0Fu);        // codes 0, 2, 4, 6
-        hi[j] = opaque((wd >> 4) & 0x0F0F0F0Fu); // codes 1, 3, 5, 7
-      } else {
-        const int d = piece - 1;
-        dst[d] = pack_bf16x2(fmaf(byte_f(lo[j], d), sc_, bi_), fmaf(byte_f(hi[j], d), sc_, bi_));
-      }
-    } else {
-      const uint32_t wd = ws.q[j][i / 2][(i % 2) * 2 + piece / 2];
-      const int e = 2 * (piece % 2);
-      dst[piece] = pack_bf16x2(fmaf(byte_f(wd, e), sc_, bi_), fmaf(byte_f(wd, e + 1), sc_, bi_));
-    }
-  };
-
-  int st0 = 0; // LDS stage of step s; s + 1 and s + 2 follow cyclically
-  for (int step = k_begin; step < k_end; ++step) {
-    const int st1 = st0 == 2 ? 0 : st0 + 1;
-    const int st2 = st1 == 2 ? 0 : st1 + 1;
-    const int wstep = min(step + 2, k_last);
-    const int xstep = min(step + 3, k_last);
-    if constexpr (SCH) {
-      const int e1 = (min(step + 1, k_last) * 64) / GS - c_cur * kCG;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        w1.s[j] = pick(cs[j], e1);
-        w1.b[j] = pick(cb[j], e1);
-      }
-      const int c2 = chunk_of(wstep);
-      if (c2 != c_cur) {
-        c_cur = c2;
-        load_chunk(c2, cs, cb);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Issue order is fixed by hand: every MFMA is followed by one small
-    // piece of other work -- a slice of the next k-step's dequantization, an
-    // LDS read refilling an A fragment, in k-step 0 the weight loads and in
-    // k-step 2 the staging store and the next activation load -- so that the
-    // matrix pipe and the VALU work side by side, global loads are spread
-    // over the step, and no wait blocks a whole batch.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = i & 1;
-      const WStep &wsrc = i < 3 ? w0 : w1;
-      const int di = i < 3 ? i + 1 : 0;
-      const uint32_t *csrc = xs + st0 * kStage;                 // this k-step's stage
-      const uint32_t *nsrc = xs + (i < 3 ? st0 : st1) * kStage; // the next k-step's
-#pragma unroll
-      for (int t = 0; t < kSlots; ++t) {
-        const int mb = t >> 1, j = t & 1;
-        acc[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[mb]), as_bf16x8(bq[c][j]), acc[mb][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        // Dequantization pieces of the next k-step, spread evenly.
-#pragma unroll
-        for (int pc = 0; pc < 2 * kPieces; ++pc)
-          if ((pc * kSlots) / (2 * kPieces) == t)
-            dq_piece(wsrc, di, pc / kPieces, pc % kPieces, bq[c ^ 1][pc / kPieces]);
-        // A fragment m is refilled kRefillLag slots after its second MFMA,
-        // once that MFMA has surely read it; the last fragments of a k-step
-        // are refilled early in the next one, before their own use.
-        if (j == 1) {
-          const int m = (((t - kRefillLag - 1) % kSlots + kSlots) % kSlots) >> 1;
-          if (t >= kRefillLag + 1)
-            a[m] = read_a(nsrc, i < 3 ? i + 1 : 0, m); // used in the next k-step
-          else
-            a[m] = read_a(csrc, i, m);                 // used later in this one
-        }
-        if (i == 2) {
-          const int q = mb;
-          if (j == 0) {
-            const int row = sr + 32 * q;
-            *reinterpret_cast<u32x4 *>(&xs[st2 * kStage + row * 32 + ((sc ^ ((row >> 1) & 7)) * 4)]) = xr[q];
-          } else {
-            xr[q] = BLoad8<XDT>::get(rx, xoff[q], uint32_t(xstep) * 64 * sizeof(XT));
-          }
-        }
-        if (i == 0 && t >= kSlots - 2) {
-          // This step's share of the weight queue: step s + 2, one 32-row
-          // block per slot.
-          const int jj = t - (kSlots - 2);
-          const uint32_t wso = uint32_t(wstep) * kWordsPerStep * 4;
-          const uint32_t sso = uint32_t((wstep * 64) / GS) * sizeof(ST);
-#pragma unroll
-          for (int v = 0; v < kWV; ++v) w2.q[jj][v] = bload16(rw, woff[jj] + 16 * v, wso);
-          if constexpr (!SCH) {
-            w2.s[jj] = BLoadScalar<SDT>::get(rs, soff[jj], sso);
-            w2.b[jj] = BLoadScalar<SDT>::get(rb, soff[jj], sso);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    w0 = w1;
-    w1 = w2;
-    st0 = st1;
-    __syncthreads();
-  }
-
-  // Output.  Accumulator entry e of lane (r, h) in tile (mb, j) is row
-  // 32*mb + 8*(e/4) + 4*h + e%4, column 32*j + r of the wave's slab: one
-  // store per element would write 2-byte pieces of two rows per instruction,
-  // and the cost of a store is per instruction.  So each wave stages its
-  // slab through its own part of the (now idle) LDS, a few 32-row blocks at
-  // a time, and writes whole 128-byte row pieces with 16-byte stores (single
-  // elements where the output rows are not 16-byte aligned).
-  using OT = typename Elem<ODT>::T;
-  constexpr int kChunkElems = 16 / int(sizeof(OT));
-  constexpr int kCpr = 64 / kChunkElems;                 // 16-byte chunks per slab row
-  constexpr int kRowBytes = 64 * int(sizeof(OT)) + 16;   // padded: no bank conflicts
-  constexpr int kWaveLds = 3 * kStage * 4 / 4;           // LDS bytes per wave
-  constexpr int kPassMB = (kWaveLds / kRowBytes) / 32 >= 4 && MB % 4 == 0 ? 4
-                          : (kWaveLds / kRowBytes) / 32 >= 2 && MB % 2 == 0 ? 2 : 1;
-  static_assert(kPassMB * 32 * kRowBytes <= kWaveLds, "output staging exceeds the LDS");
-  auto store_tile = [&](auto produce) {
-    const bool vec = N % kChunkElems == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
-    uint8_t *wl = reinterpret_cast<uint8_t *>(xs) + wave * kWaveLds;
-#pragma unroll
-    for (int p0 = 0; p0 < MB; p0 += kPassMB) {
-#pragma unroll
-      for (int mb = p0; mb < p0 + kPassMB; ++mb) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float v[16];
-          produce(mb, j, v);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int row = 32 * (mb - p0) + 8 * (e / 4) + 4 * h + (e % 4);
-            *reinterpret_cast<OT *>(wl + row * kRowBytes + (32 * j + r) * int(sizeof(OT))) =
-                Elem<ODT>::store(v[e]);
-          }
-        }
-      }
-      // The slab is read back by other lanes of this wave only.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int it = 0; it < kPassMB * 32 * kCpr / 64; ++it) {
-        const int idx = it * 64 + lane;
-        const int row = idx / kCpr, chunk = idx % kCpr;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(wl + row * kRowBytes + chunk * 16);
-        const int grow = m0 + 32 * p0 + row;
-        const int gcol = nw + chunk * kChunkElems;
-        if (grow < M) {
-          OT *dst = y + int64_t(grow) * N + gcol;
-          if (vec) {
-            if (gcol < N) *reinterpret_cast<u32x4 *>(dst) = v;
-          } else {
-            // Rows not 16-byte aligned, or a ragged last chunk: element stores.
-#pragma unroll
-            for (int q = 0; q < kChunkElems; ++q) {
-              if (gcol + q < N) {
-                const uint32_t word = v[(q * int(sizeof(OT))) / 4];
-                if constexpr (sizeof(OT) == 4)
-                  dst[q] = __builtin_bit_cast(OT, word);
-                else
-                  dst[q] = OT((q & 1) ? (word >> 16) : (word & 0xffffu));
-              }
-            }
-          }
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-  };
-
-  if (bid >= wk.dp_tiles) {
-    // A K range of a split tile: its f32 accumulators go to the workspace in
-    // 16-byte pieces, register-major: entries 4q..4q+3 of MFMA tile (mb, j)
-    // of thread t at float4 ((mb*2 + j)*4 + q)*256 + t of the range's slot,
-    // so each store instruction writes 1 KB contiguous per wave.  Rows past M
-    // are written too and never read.  The reduction kernel that follows on
-    // the stream adds the ranges in order.
-    const int64_t slot = int64_t(tile - wk.dp_tiles) * wk.splits + split;
-    float4 *mine = reinterpret_cast<float4 *>(wk.partial + slot * (BM * kTileN)) + tid;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          mine[((mb * 2 + j) * 4 + q) * kThreads] =
-              float4{acc[mb][j][4 * q], acc[mb][j][4 * q + 1], acc[mb][j][4 * q + 2], acc[mb][j][4 * q + 3]};
-    return;
-  }
-
-  // The epilogue needs only the column's bias: one value per lane per 32-row
-  // block of weights.  The activation is chosen once for the whole tile: a
-  // per-element branch would end each element's LDS write in a wait.
-  float bcol[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
-  auto finish = [&](auto act) {
-    store_tile([&](int mb, int j, float (&v)[16]) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float t = acc[mb][j][e] + bcol[j];
-        v[e] = decltype(act)::value ? gelu_approx_f(t) : t;
-      }
-    });
-  };
-  if (ep.act == 1)
-    finish(std::integral_constant<bool, true>{});
-  else
-    finish(std::integral_constant<bool, false>{});
-}
-
-// Sum of the K ranges of the split tiles, in range order (so the result does
-// not depend on which block finished first), with the epilogue, converted to
-// the output type.  Thread i of the launch takes float4 i of the partial
-// layout: four consecutive rows of one column (accumulator entries 4q..4q+3
-// of one MFMA tile of one tile-kernel thread).
-template <int ODT>
-__global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
-                                                         const float *__restrict__ partial,
-                                                         int M, int N, int bm, int tiles_n,
-                                                         int dp_tiles, int splits,
-                                                         kern::Epilogue ep) {
-  const int per_tile = bm * (kTileN / 4); // float4 pieces of one partial tile
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int sk = int(idx / per_tile);
-  const int within = int(idx % per_tile);
-  const int reg4 = within / kThreads;      // (mb*2 + j)*4 + q
-  const int t = within % kThreads;         // the tile kernel's thread
-  const int lane = t & 63, wave = t >> 6;
-  const int mb = reg4 >> 3, j = (reg4 >> 2) & 1, q = reg4 & 3;
-  const int row = 32 * mb + 8 * q + 4 * (lane >> 5);  // first of four rows
-  const int col = wave * 64 + 32 * j + (lane & 31);
-  const int tile = dp_tiles + sk;
-  const int grow = (tile / tiles_n) * bm + row;
-  const int gcol = (tile % tiles_n) * kTileN + col;
-  if (grow >= M || gcol >= N) return;
-  const float4 *src = reinterpret_cast<const float4 *>(partial) + int64_t(sk) * splits * per_tile + within;
-  float4 sum = src[0];
-  for (int p0 = 1; p0 < splits; p0 += 4) {
-    float4 v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (p0 + u < splits) v[u] = src[int64_t(p0 + u) * per_tile];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (p0 + u < splits) {
-        sum.x += v[u].x;
-        sum.y += v[u].y;
-        sum.z += v[u].z;
-        sum.w += v[u].w;
-      }
-  }
-  const float b = epi_bias(ep, gcol);
-  const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-    if (grow + u < M) y[int64_t(grow + u) * N + gcol] = Elem<ODT>::store(epi_apply(ep, s4[u], b));
-}
-
-template <int BITS, int XDT, int SDT, int ODT, int BM>
-void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
-                  const void *s, const void *b, int M, int N, int K, int gs,
-                  const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
-                  const kern::Epilogue &ep, hipStream_t st) {
-  const QmmWork wk{plan.tiles_n, plan.dp_tiles, plan.splits, plan.steps_per_split, ws.partial};
-  const dim3 grid(plan.blocks);
-  auto *yp = static_cast<typename Elem<ODT>::T *>(y);
-  auto *xp = static_cast<const typename Elem<XDT>::T *>(x);
-  auto *sp = static_cast<const typename Elem<SDT>::T *>(s);
-  auto *bp = static_cast<const typename Elem<SDT>::T *>(b);
-  // Chunked scale loads need every scale row 16-byte aligned.
-  const size_t srow_bytes = size_t(K / gs) * sizeof(typename Elem<SDT>::T);
-  const bool sch = srow_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(s) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(b) % 16 == 0;
-#define SDQ_QMM_LAUNCH(G, C) \
-  qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk, ep)
-  if (gs == 64) {
-    if (sch) SDQ_QMM_LAUNCH(64, true);
-    else SDQ_QMM_LAUNCH(64, false);
-  } else {
-    if (sch) SDQ_QMM_LAUNCH(128, true);
-    else SDQ_QMM_LAUNCH(128, false);
-  }
-#undef SDQ_QMM_LAUNCH
-  const int sk_tiles = plan.tiles - plan.dp_tiles;
-  if (sk_tiles > 0) {
-    hip_check(hipGetLastError(), "qmm launch");
-    const int64_t threads = int64_t(sk_tiles) * BM * (kTileN / 4);
-    qmm_reduce_kernel<ODT><<<dim3(unsigned(threads / 256)), 256, 0, st>>>(
-        yp, ws.partial, M, N, BM, plan.tiles_n, plan.dp_tiles, plan.splits, ep);
-  }
-}
-
-template <int BITS, int XDT, int SDT, int ODT>
-void launch_qmm_bm(void *y, const void *x, int64_t ldx, const uint32_t *w,
-                   const void *s, const void *b, int M, int N, int K, int gs,
-                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
-                   const kern::Epilogue &ep, hipStream_t st) {
-  if (plan.bm == 128)
-    launch_qmm_t<BITS, XDT, SDT, ODT, 128>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
-  else
-    launch_qmm_t<BITS, XDT, SDT, ODT, 256>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
-}
-
-#define SDQ_QMM_CASE(XD, SD, OD)                                                         \
-  if (x_dtype == XD && s_dtype == SD && y_dtype == OD) {                                 \
-    if (bits == 4)                                                                       \
-      launch_qmm_bm<4, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K),  \
-                                   group_size, plan, ws, ep, stream);                    \
-    else                                                                                 \
-      launch_qmm_bm<8, XD, SD, OD>(y, x, ldx, w, scales, biases, int(M), int(N), int(K),  \
-                                   group_size, plan, ws, ep, stream);                    \
-    hip_check(hipGetLastError(), "qmm launch");                                          \
-    return;                                                                              \
+namespace {
+#define SDQ_QMM_CASE(XD, SD, OD)                                                           \
+  if (x_dtype == XD && s_dtype == SD && y_dtype == OD) {                                   \
+    qmm_detail::qmm_combo<XD, SD, OD>(bits, y, x, ldx, w, scales, biases, int(M), int(N),  \
+                                      int(K), group_size, plan, ws, ep, stream);           \
+    hip_check(hipGetLastError(), "qmm launch");                                            \
+    return;                                                                                \
   }
 
 } // namespace
@@ -585,7 +41,7 @@ namespace kern {
 QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
   QmmPlan p;
   p.bm = M <= 128 ? 128 : 256;
-  p.tiles_n = int((N + kTileN - 1) / kTileN);
+  p.tiles_n = int((N + qmm_detail::kTileN - 1) / qmm_detail::kTileN);
   const int64_t tiles_m = (M + p.bm - 1) / p.bm;
   p.tiles = int(tiles_m * p.tiles_n);
   const int64_t steps = K / 64;
@@ -619,7 +75,7 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
   }
   const int64_t sk_tiles = p.tiles - p.dp_tiles;
   p.blocks = int(p.dp_tiles + sk_tiles * p.splits);
-  p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * size_t(p.bm) * kTileN;
+  p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * size_t(p.bm) * qmm_detail::kTileN;
   return p;
 }
 

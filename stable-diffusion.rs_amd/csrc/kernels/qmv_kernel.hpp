@@ -1,0 +1,461 @@
+// qmv_kernel.hpp -- y = x @ dequantize(w).T for few rows of x (M <= 32): the
+// bandwidth-bound decode/modulation shape of mlx_quantized_matmul
+// (crates/sd-tensor/src/mlx.rs:386-397, 1947-1975; callers e.g. the Flux
+// modulation linears at M = 1, sd-models/src/mlx/flux.rs:279-299, 437, and the
+// T5 FFN at few tokens, t5.rs:209-214).
+//
+// Time here is the packed weight stream, so the kernel is laid out as a
+// stream with little work per byte and nothing serialised behind it:
+//
+//   * A block owns T tiles of 16 weight rows (output columns) and all of K.
+//     Its T*S waves each stream one tile over one of S contiguous K ranges;
+//     at the end the S waves of a tile add their partial tiles through LDS in
+//     range order (deterministic) and the first applies the epilogue and
+//     stores.  No partial result leaves the block and there is no second pass.
+//   * Each wave stages the scales and biases of its 16 rows and K range in
+//     its own LDS region, as (s, b - OFF*s) pairs, and -- at M <= 4 -- its
+//     slice of x as bf16 (XMode kXWave): no block-wide barrier stands between
+//     a wave and its stream.  For larger M with a small x the block stages x
+//     once for all its tiles (kXBlock); otherwise each wave reads its
+//     activation fragments per chunk from global memory (kXDirect).
+//   * MFMA v_mfma_f32_16x16x32_bf16 with the weight rows on its N side and
+//     the tokens on its M side (16 rows per MFMA row block, two blocks for
+//     M <= 32).  Lane (n, h) = (lane % 16, lane / 16) supplies weight row n
+//     and token row n of the row block.  Codes are loaded 16 bytes per lane,
+//     16 rows x 64 bytes per load instruction, in chunks of 128 K:
+//       4-bit: one load per chunk; lane h holds K [32h, 32h + 32) as four
+//       words.  A 4 x 4 transpose of words across the four lane groups
+//       (v_permlane32_swap, then v_permlane16_swap) leaves word i of lane h
+//       holding K [32i + 8h, 32i + 8h + 8), so MFMA i of the chunk covers K
+//       [32i, 32i + 32) -- inside group i / 2.
+//       8-bit: two loads per chunk (one per group); MFMA i takes words
+//       2i, 2i + 1, i.e. K [64(i/2) + 16h + 8(i%2), +8).
+//   * Codes are never dequantized element by element.  The MFMA multiplies x
+//     by c_k = q_k + OFF held EXACTLY in bf16 (4-bit: OFF = 128, the pattern
+//     0x43nn built by byte permutes; 8-bit: OFF = 0, q converted), giving
+//     t[m][n] = sum_k x[m,k] c_k per group, and a second MFMA against ones
+//     gives the group sums X[m] = sum_k x[m,k] in the same lane layout.  Then
+//     y += s t + (b - OFF s) X: the affine dequantization is applied once per
+//     group per output, in f32, which is more accurate than rounding each
+//     dequantized weight to bf16.
+//   * kDepth chunks of loads are in flight per wave.  Chunks past a wave's
+//     range are addressed beyond the buffer's end: such loads return zeros
+//     without touching memory.
+#pragma once
+
+#include <algorithm>
+
+#include "device_common.hpp"
+#include "launch.hpp"
+#include "qmv_lds.hpp"
+
+#include "../sdq_internal.hpp"
+
+namespace sdq {
+namespace qmv_detail {
+
+using namespace dev;
+
+constexpr int kDepth = 2;       // 128-wide chunks in flight per wave (default)
+constexpr uint32_t kOob = 0x80000000u; // an offset past every buffer (all are < 2 GiB)
+
+// v_permlane32_swap: lanes 32-63 of a trade places with lanes 0-31 of b.
+__device__ __forceinline__ void perm32_swap(uint32_t &a, uint32_t &b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+// v_permlane16_swap: the odd 16-lane rows of a trade places with the even
+// rows of b.
+__device__ __forceinline__ void perm16_swap(uint32_t &a, uint32_t &b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+// MFMA B operand for eight 4-bit codes (one word, first code in the low bits)
+// in natural K order, each as the exact bf16 value 128 + q (pattern 0x43nn):
+// split into even and odd codes, interleave them back into code order, then
+// pair each code byte with the constant exponent byte 0x43.
+__device__ __forceinline__ u32x4 codes4_b(uint32_t wd) {
+  const uint32_t lo = wd & 0x0F0F0F0Fu;        // c0 c2 c4 c6
+  const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu; // c1 c3 c5 c7
+  const uint32_t m0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u); // c0 c1 c2 c3
+  const uint32_t m1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u); // c4 c5 c6 c7
+  const uint32_t k43 = 0x43434343u;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(k43, m0, 0x04010400u); // (c0, c1)
+  r[1] = __builtin_amdgcn_perm(k43, m0, 0x04030402u); // (c2, c3)
+  r[2] = __builtin_amdgcn_perm(k43, m1, 0x04010400u); // (c4, c5)
+  r[3] = __builtin_amdgcn_perm(k43, m1, 0x04030402u); // (c6, c7)
+  return r;
+}
+
+// Eight 8-bit codes (two words), in element order, as exact bf16 values q.
+__device__ __forceinline__ u32x4 codes8_b(uint32_t w0, uint32_t w1) {
+  const uint32_t a = opaque(w0), b = opaque(w1);
+  u32x4 r;
+  r[0] = pack_bf16x2(float(a & 0xffu), float((a >> 8) & 0xffu));
+  r[1] = pack_bf16x2(float((a >> 16) & 0xffu), float(a >> 24));
+  r[2] = pack_bf16x2(float(b & 0xffu), float((b >> 8) & 0xffu));
+  r[3] = pack_bf16x2(float((b >> 16) & 0xffu), float(b >> 24));
+  return r;
+}
+
+__device__ __forceinline__ floatx4 mfma16(const u32x4 &a, const u32x4 &b, const floatx4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// K offset, within a 128-wide chunk, of lane group h's eight slots of MFMA i.
+template <int BITS> __device__ __forceinline__ int slot_k(int i, int h) {
+  return BITS == 4 ? 32 * i + 8 * h : 64 * (i >> 1) + 16 * h + 8 * (i & 1);
+}
+
+// One chunk's loads: the lane's codes and, when x is read directly, its
+// activation fragments (MFMA i of row block mb).
+template <int BITS, int MB, bool XD> struct Chunk {
+  u32x4 q[BITS / 4];
+  u32x4 a[XD ? MB : 1][XD ? 4 : 1];
+};
+
+// MB: 16-token MFMA row blocks (M <= 16 * MB).  GS: group size (64 or 128).
+// XM: where x comes from (XMode).  Launch: grid = ceil(tiles / T), T * S waves.
+template <int BITS, int XDT, int SDT, int ODT, int MB, int GS, int XM, int DEPTH = kDepth>
+__global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
+    typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
+    int64_t ldx, const uint32_t *__restrict__ w,
+    const typename Elem<SDT>::T *__restrict__ scales,
+    const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, int T, int S,
+    kern::Epilogue ep) {
+  using XT = typename Elem<XDT>::T;
+  using ST = typename Elem<SDT>::T;
+  constexpr bool kXD = XM == kXDirect;
+  constexpr float kOff = BITS == 4 ? 128.0f : 0.0f;
+  constexpr int kChunkBytes = 128 * BITS / 8; // one row's codes per chunk
+  constexpr int kGpc = 128 / GS;              // groups per chunk (1 or 2)
+
+  const int wave = int(threadIdx.x) >> 6;
+  const int lane = int(threadIdx.x) & 63;
+  const int ln = lane & 15;
+  const int lh = lane >> 4;
+  const int tl = wave / S;      // tile of this block
+  const int rs = wave - tl * S; // K range of the tile
+  const int tiles = (N + 15) / 16;
+  const int tile = int(blockIdx.x) * T + tl;
+  const bool live = tile < tiles;
+  const int n = tile * 16 + ln;
+  const int nrow = min(n, N - 1); // rows past N are read, never stored
+  const int groups = K / GS;
+
+  // This wave's chunks [c0, c1) of the 128-wide chunks and groups [g0, g1);
+  // the last chunk is half when K % 128 == 64 (group size 64).
+  const int nchunk = (K + 127) / 128;
+  const int c0 = int((int64_t(nchunk) * rs) / S);
+  const int c1 = int((int64_t(nchunk) * (rs + 1)) / S);
+  const int ncs = live ? c1 - c0 : 0;
+  const bool half_tail = (K & 127) != 0;
+  const int g0 = c0 * kGpc;
+  const int gw = min(c1 * kGpc, groups) - g0;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const QmvLds L = qmv_lds(XM, M, K, GS, T, S, MB);
+  unsigned char *wreg = smem + L.wave + wave * L.wave_bytes;
+  float2 *sbw = reinterpret_cast<float2 *>(wreg);                 // [16][L.gw]
+  uint16_t *xl = reinterpret_cast<uint16_t *>(XM == kXBlock ? smem + L.x : wreg + L.wsb);
+  floatx4 *red = reinterpret_cast<floatx4 *>(smem + L.red);
+
+  // Buffer windows: byte offsets fit in 32 bits (checked on the host).
+  const Rsrc rw = make_rsrc(w, uint32_t(int64_t(N) * K * BITS / 8));
+  const uint32_t woff = uint32_t(int64_t(nrow) * K * BITS / 8) + uint32_t(16 * lh);
+  const Rsrc rx = make_rsrc(x, uint32_t((int64_t(M - 1) * ldx + K) * sizeof(XT)));
+  const Rsrc rs_ = make_rsrc(scales, uint32_t(int64_t(N) * groups * sizeof(ST)));
+  const Rsrc rb_ = make_rsrc(biases, uint32_t(int64_t(N) * groups * sizeof(ST)));
+  uint32_t xoff[MB];
+  int xrow[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    xrow[mb] = min(mb * 16 + ln, M - 1); // rows past M repeat row M - 1, never stored
+    xoff[mb] = uint32_t(int64_t(xrow[mb]) * ldx * sizeof(XT));
+  }
+
+  auto load = [&](int i, Chunk<BITS, MB, kXD> &q) {
+    // Local chunk i of this wave; past the range every load is out of bounds.
+    const bool in = i < ncs;
+    const int c = c0 + i;
+    const uint32_t cw = in ? uint32_t(c) * kChunkBytes : kOob;
+#pragma unroll
+    for (int v = 0; v < BITS / 4; ++v) q.q[v] = bload16(rw, woff + 64 * v, cw);
+    if constexpr (kXD) {
+      const uint32_t cx = in ? uint32_t(c) * 128 * uint32_t(sizeof(XT)) : kOob;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          q.a[mb][j] = BLoad8<XDT>::get(rx, xoff[mb] + slot_k<BITS>(j, lh) * uint32_t(sizeof(XT)), cx);
+    }
+  };
+
+  // 1. Staging.  The wave's own staging loads (scale/bias pairs of its 16
+  //    rows and groups; kXWave: its slice of x) go out first, then the first
+  //    chunks' code loads, then the staging is stored: the wait for the
+  //    staging does not include the codes (the load counter retires in issue
+  //    order), which keep streaming.
+  Chunk<BITS, MB, kXD> ring[DEPTH];
+  {
+    // Lane (r, p) = (lane % 16, lane / 16) takes groups g0 + p + 4i of row
+    // r: each load instruction reads 16 rows x 4 consecutive groups.
+    constexpr int kSbIter = 4; // 16 groups per row per batch
+    const int srow = min(int(blockIdx.x) * T * 16 + tl * 16 + ln, N - 1);
+    const uint32_t sbase = uint32_t(int64_t(srow) * groups * sizeof(ST));
+    constexpr int kXIter = kXWaveMaxChunks * 16 / 64; // x pieces per lane and row (kXWave)
+    u32x4 xv[XM == kXWave ? 4 : 1][kXIter];
+    for (int gb = 0; gb < gw || gb == 0; gb += 4 * kSbIter) {
+      float sv[kSbIter], bv[kSbIter];
+#pragma unroll
+      for (int i = 0; i < kSbIter; ++i) {
+        const int g = gb + lh + 4 * i;
+        const uint32_t off = g < gw ? uint32_t(g0 + g) * uint32_t(sizeof(ST)) : kOob;
+        sv[i] = BLoadScalar<SDT>::get(rs_, sbase, off);
+        bv[i] = BLoadScalar<SDT>::get(rb_, sbase, off);
+      }
+      if (gb == 0) {
+        if constexpr (XM == kXWave) {
+          // Rows m < M (M <= 4) of columns [128 c0, 128 c1), eight per piece.
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < kXIter; ++j) {
+              const int pc = lane + 64 * j;
+              const bool in = m < M && pc < ncs * 16;
+              const uint32_t off = in ? uint32_t((int64_t(m) * ldx + c0 * 128 + 8 * pc) * sizeof(XT)) : kOob;
+              xv[m][j] = BLoad8<XDT>::get(rx, off, 0);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+        if constexpr (XM == kXWave) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < kXIter; ++j) {
+              const int pc = lane + 64 * j;
+              if (m < M && pc < ncs * 16)
+                *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * pc) = xv[m][j];
+            }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSbIter; ++i) {
+        const int g = gb + lh + 4 * i;
+        if (g < gw) sbw[ln * L.gw + g] = make_float2(sv[i], fmaf(-kOff, sv[i], bv[i]));
+      }
+    }
+    if constexpr (XM == kXBlock) {
+      // The block stages all of x, eight values per piece, for its T tiles.
+      constexpr int kXLoads = 8;
+      const int nthreads = int(blockDim.x);
+      const int tid = int(threadIdx.x);
+      const int per_row = K / 8;
+      const int x_pieces = M * per_row;
+      // Row of piece e: a float estimate corrected once (exact: the
+      // estimate is off by at most one for these sizes).
+      const float inv_per_row = 1.0f / float(per_row);
+      auto x_row = [&](int e) {
+        int m = int(float(e) * inv_per_row);
+        m -= m * per_row > e;
+        m += (m + 1) * per_row <= e;
+        return m;
+      };
+      for (int base = 0; base < x_pieces; base += kXLoads * nthreads) {
+        u32x4 v[kXLoads];
+#pragma unroll
+        for (int j = 0; j < kXLoads; ++j) {
+          const int e = min(base + j * nthreads + tid, x_pieces - 1);
+          const int m = x_row(e);
+          v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + 8 * (e - m * per_row));
+        }
+#pragma unroll
+        for (int j = 0; j < kXLoads; ++j) {
+          const int e = base + j * nthreads + tid;
+          if (e < x_pieces) {
+            const int m = x_row(e);
+            *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * (e - m * per_row)) = v[j];
+          }
+        }
+      }
+      __syncthreads();
+    } else {
+      // The stage is this wave's own: a wave-scope fence orders it.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // 2. Stream the chunks.
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  floatx4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = zero;
+  const float2 *sbrow = sbw + ln * L.gw;
+  // Column of chunk c's K range within the staged x rows.
+  const int xcol0 = XM == kXBlock ? 0 : c0 * 128;
+
+  for (int base = 0; base < ncs; base += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int i = base + d;
+      Chunk<BITS, MB, kXD> &q = ring[d];
+      if (i < ncs) {
+        const int c = c0 + i;
+        u32x4 bq[4];
+        if constexpr (BITS == 4) {
+          uint32_t w0 = q.q[0][0], w1 = q.q[0][1], w2 = q.q[0][2], w3 = q.q[0][3];
+          perm32_swap(w0, w2);
+          perm32_swap(w1, w3);
+          perm16_swap(w0, w1);
+          perm16_swap(w2, w3);
+          bq[0] = codes4_b(w0);
+          bq[1] = codes4_b(w1);
+          bq[2] = codes4_b(w2);
+          bq[3] = codes4_b(w3);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bq[j] = codes8_b(q.q[j >> 1][2 * (j & 1)], q.q[j >> 1][2 * (j & 1) + 1]);
+        }
+        // The chunk's MFMAs, group by group: t = sum x c, xs = sum x.
+        const bool two = !(half_tail && c == nchunk - 1); // second half of the chunk exists
+#pragma unroll
+        for (int gg = 0; gg < kGpc; ++gg) {
+          if (gg == 1 && !two) break;
+          constexpr int kPer = 4 / kGpc; // MFMAs per group in this chunk
+          floatx4 t[MB], xs[MB];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+              const int mi = gg * kPer + j;
+              u32x4 a;
+              if constexpr (kXD) {
+                a = q.a[mb][mi];
+              } else {
+                a = *reinterpret_cast<const u32x4 *>(xl + xrow[mb] * L.xstride + c * 128 - xcol0 +
+                                                     slot_k<BITS>(mi, lh));
+              }
+              t[mb] = mfma16(a, bq[mi], j == 0 ? zero : t[mb]);
+              xs[mb] = mfma16(a, ones, j == 0 ? zero : xs[mb]);
+            }
+          }
+          const float2 sc = sbrow[i * kGpc + gg];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              acc[mb][e] = fmaf(sc.x, t[mb][e], acc[mb][e]);
+              acc[mb][e] = fmaf(sc.y, xs[mb][e], acc[mb][e]);
+            }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load(i + DEPTH, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // 3. The S partial tiles of each tile are added in range order.
+  if (S > 1) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) red[(wave * MB + mb) * 64 + lane] = acc[mb];
+    __syncthreads();
+    if (rs != 0) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      floatx4 sum = red[((tl * S) * MB + mb) * 64 + lane];
+      for (int v = 1; v < S; ++v) {
+        const floatx4 p = red[((tl * S + v) * MB + mb) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += p[e];
+      }
+      acc[mb] = sum;
+    }
+  }
+
+  // Accumulator entry e of lane (n, h) in row block mb is token
+  // 16 mb + 4 h + e, output column n of the tile.
+  if (!live || n >= N) return;
+  const float bn = epi_bias(ep, n);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = mb * 16 + 4 * lh + e;
+      if (m < M)
+        y[int64_t(m) * N + n] = Elem<ODT>::store(epi_combine(ep, epi_apply(ep, acc[mb][e], bn), m, n));
+    }
+}
+
+template <int BITS, int XDT, int SDT, int ODT, int MB, int GS, int XM, int DEPTH = kDepth>
+void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
+                  const void *b, int M, int N, int K, const kern::QmvPlan &plan,
+                  const kern::Epilogue &ep, hipStream_t st) {
+  const int tiles = (N + 15) / 16;
+  const int T = plan.tiles_per_block;
+  const QmvLds l = qmv_lds(XM, M, K, GS, T, plan.waves, MB);
+  const dim3 grid(unsigned((tiles + T - 1) / T));
+  qmv_kernel<BITS, XDT, SDT, ODT, MB, GS, XM, DEPTH><<<grid, 64 * T * plan.waves, l.total, st>>>(
+      static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
+      w, static_cast<const typename Elem<SDT>::T *>(s), static_cast<const typename Elem<SDT>::T *>(b),
+      M, N, K, T, plan.waves, ep);
+}
+
+// One activation/scale/output dtype combination of the kernel, for 4 or 8
+// bits: instantiated once per combination in its own translation unit
+// (qmv_inst.hip, compiled once per combination) so the build runs in parallel.
+template <int XD, int SD, int OD>
+void qmv_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
+               const void *b, int M, int N, int K, int gs, const kern::QmvPlan &plan,
+               const kern::Epilogue &ep, hipStream_t st);
+
+template <int BITS, int XD, int SD, int OD, int XM>
+void qmv_xm(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s, const void *b,
+            int M, int N, int K, int gs, const kern::QmvPlan &plan, const kern::Epilogue &ep,
+            hipStream_t st) {
+  if (gs == 64) {
+    if (plan.row_blocks == 1)
+      launch_qmv_t<BITS, XD, SD, OD, 1, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+    else
+      launch_qmv_t<BITS, XD, SD, OD, 2, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+  } else {
+    if (plan.row_blocks == 1)
+      launch_qmv_t<BITS, XD, SD, OD, 1, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+    else
+      launch_qmv_t<BITS, XD, SD, OD, 2, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+  }
+}
+
+template <int BITS, int XD, int SD, int OD>
+void qmv_bits(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s, const void *b,
+              int M, int N, int K, int gs, const kern::QmvPlan &plan, const kern::Epilogue &ep,
+              hipStream_t st) {
+  if (plan.xmode == kXWave)
+    qmv_xm<BITS, XD, SD, OD, kXWave>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+  else if (plan.xmode == kXBlock)
+    qmv_xm<BITS, XD, SD, OD, kXBlock>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+  else
+    qmv_xm<BITS, XD, SD, OD, kXDirect>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+}
+
+template <int XD, int SD, int OD>
+void qmv_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
+               const void *b, int M, int N, int K, int gs, const kern::QmvPlan &plan,
+               const kern::Epilogue &ep, hipStream_t st) {
+  if (bits == 4)
+    qmv_bits<4, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+  else
+    qmv_bits<8, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+}
+
+} // namespace qmv_detail
+} // namespace sdq

@@ -36,24 +36,46 @@ int promote_float(int a, int b); // MLX promotion among the three float types
 
 // ---- device memory ------------------------------------------------------
 
-// One device allocation.  When the last reference goes, the block returns to
-// the allocator's cache, tagged with the stream that last used it: reuse on
-// that stream is ordered by the stream; reuse on another first waits for it.
+// One device allocation.  `stream` is the stream it was allocated for (its
+// producer); `readers` are the other streams that were ordered to use it
+// (note_reader, called by the ops that consume it elsewhere).  When the last
+// reference goes, one event per such stream is recorded and the block returns
+// to the allocator's cache carrying them: whichever stream reuses the block
+// first waits on all of them (a device-side wait, no host synchronisation),
+// so no stream can overwrite data another stream is still reading.
 struct Buffer {
   void *ptr = nullptr;
   size_t capacity = 0;
   int device = 0;
   hipStream_t stream = nullptr;
+  std::vector<hipStream_t> readers;
+  void note_reader(hipStream_t s);
   ~Buffer();
 };
 
 std::shared_ptr<Buffer> allocate(size_t bytes, int device, hipStream_t stream);
+// True for a stream of sdq_gpu_stream_new that sdq_stream_free has destroyed.
+// Such a stream is synchronised before it is destroyed, so its work is known
+// to be complete and nothing waits on it afterwards.
+bool stream_retired(hipStream_t s);
 size_t active_memory();
 size_t peak_memory();
 size_t cache_memory();
 void reset_peak_memory();
 size_t set_cache_limit(size_t limit); // returns the previous limit
 void clear_cache();
+
+// ---- per-stream workspace ---------------------------------------------------
+
+// Scratch memory of the large-M kernel (f32 partial tiles when it splits K
+// across blocks), one buffer per (device, stream): calls on one stream are
+// ordered by it, so they share the memory with no synchronisation and no
+// per-call allocation.  It grows to the largest request and is kept until
+// the stream is freed (release_stream_workspace) or the cache is cleared.
+// The per-thread handle hipStreamPerThread names a different stream in each
+// host thread, so its workspace is kept per thread.
+float *stream_workspace(int device, hipStream_t stream, size_t partial_floats);
+void release_stream_workspace(int device, hipStream_t stream);
 
 // ---- streams ------------------------------------------------------------
 

@@ -14,9 +14,12 @@
 namespace sdq {
 namespace {
 
-// Waits on `s` for the work that produced `a`, when that ran elsewhere.
+// Waits on `s` for the work that produced `a`, when that ran elsewhere, and
+// records `s` as a user of a's memory, so that the allocator orders a later
+// reuse of the block after this use too.
 void order_after(const ArrayImpl *a, const StreamImpl *s) {
-  if (!a->stream || a->stream == s->stream) return;
+  if (a->buf && a->buf->ptr) a->buf->note_reader(s->stream);
+  if (!a->stream || a->stream == s->stream || stream_retired(a->stream)) return;
   hipEvent_t ev;
   hip_check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate");
   hip_check(hipEventRecord(ev, a->stream), "hipEventRecord");
@@ -62,56 +65,25 @@ int cu_count(int device) {
   return n;
 }
 
-// Per-stream split-K counters: zeroed once when (re)allocated; every kernel
-// that uses them leaves them zero again.
-unsigned *split_counters(int device, hipStream_t stream, int needed) {
-  struct Slot {
-    std::shared_ptr<Buffer> buf;
-    int count = 0;
-  };
-  static std::mutex mu;
-  static std::map<hipStream_t, Slot> slots;
-  std::lock_guard<std::mutex> lock(mu);
-  Slot &slot = slots[stream];
-  if (slot.count < needed) {
-    const int count = std::max(needed, 4096);
-    auto buf = allocate(size_t(count) * sizeof(unsigned), device, stream);
-    hip_check(hipMemsetAsync(buf->ptr, 0, size_t(count) * sizeof(unsigned), stream),
-              "hipMemsetAsync");
-    slot.buf = buf;
-    slot.count = count;
-  }
-  return static_cast<unsigned *>(slot.buf->ptr);
-}
-
 // y = x @ dequantize(w).T on device pointers; picks the kernel by M.
 void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
                      const uint32_t *w, const void *scales, const void *biases,
                      int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
-                     int device, hipStream_t stream,
-                     std::shared_ptr<Buffer> *keep_alive, const kern::Epilogue &ep = {}) {
+                     int device, hipStream_t stream, const kern::Epilogue &ep = {}) {
   if (M == 0 || N == 0) return;
   if (gs != 64 && gs != 128)
     fail("the quantized matmul kernels take group size 64 or 128, got " + std::to_string(gs));
   if (bits != 4 && bits != 8)
     fail("the quantized matmul kernels take 4 or 8 bits, got " + std::to_string(bits));
   if (M <= 32) {
-    kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, bits, cu_count(device));
-    kern::SplitWorkspace ws;
-    if (plan.splits > 1) {
-      *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
-      ws.partial = static_cast<float *>((*keep_alive)->ptr);
-      ws.counters = split_counters(device, stream, plan.counters);
-    }
+    const kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, bits, cu_count(device));
     kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ws, ep, stream);
+              plan, ep, stream);
   } else {
     kern::QmmPlan plan = kern::plan_qmm(M, N, K, cu_count(device));
     kern::SplitWorkspace ws;
-    if (plan.dp_tiles < plan.tiles) {
-      *keep_alive = allocate(plan.partial_floats * sizeof(float), device, stream);
-      ws.partial = static_cast<float *>((*keep_alive)->ptr);
-    }
+    if (plan.dp_tiles < plan.tiles)
+      ws.partial = stream_workspace(device, stream, plan.partial_floats);
     // The tile kernel fuses bias and activation; the combine stage follows
     // as one in-place pass (the tile store with it grows the kernel ~6x).
     kern::Epilogue ep_mm = ep;
@@ -328,10 +300,9 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
     oshape.back() = int(N);
     auto out = make_array(oshape, out_dtype, *st);
     const int64_t M = K ? int64_t(xa->size / size_t(K)) : 0;
-    std::shared_ptr<Buffer> scratch;
     matmul_dispatch(out->data(), out_dtype, xa->data(), xa->dtype, K,
                     static_cast<const uint32_t *>(wa->data()), sa->data(), ba->data(), sa->dtype,
-                    M, N, K, gs, nb, st->device, st->stream, &scratch, ep);
+                    M, N, K, gs, nb, st->device, st->stream, ep);
     set_result(res, std::move(out));
 }
 
@@ -384,9 +355,8 @@ int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, i
     if (M > 0 && N > 0 && (!y || !x || !w || !scales || !biases)) fail("NULL pointer argument");
     int device = 0;
     hip_check(hipGetDevice(&device), "hipGetDevice");
-    std::shared_ptr<Buffer> scratch;
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
-                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch);
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream));
   });
 }
 
@@ -413,9 +383,8 @@ int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x, int x
     ep.bias_dtype = bias ? bias_dtype : 0;
     ep.act = activation;
     if (!kern::epilogue_ok(ep)) fail("bad epilogue");
-    std::shared_ptr<Buffer> scratch;
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
-                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), &scratch, ep);
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), ep);
   });
 }
 

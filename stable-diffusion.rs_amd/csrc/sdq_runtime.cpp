@@ -9,7 +9,9 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <sstream>
+#include <thread>
 
 #include "sdq_internal.hpp"
 
@@ -111,14 +113,38 @@ int promote_float(int a, int b) {
 
 namespace {
 
+// Makes `device` current for the scope (the allocator is called from any
+// thread, with any device current).
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev) != hipSuccess) {
+      (void)hipGetLastError();
+      prev = -1;
+    }
+    if (prev != device) (void)hipSetDevice(device);
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+// An event recorded on `stream` when a block was freed: a later user of the
+// block on another stream waits for it.
+struct Pending {
+  hipEvent_t event;
+  hipStream_t stream;
+};
+
 struct FreeBlock {
   void *ptr;
   size_t capacity;
-  hipStream_t stream;
+  std::vector<Pending> pending;
 };
 
 struct DevicePool {
   std::multimap<size_t, FreeBlock> free_blocks; // by capacity
+  std::vector<hipEvent_t> events;               // recycled, timing disabled
 };
 
 struct Pool {
@@ -135,6 +161,27 @@ Pool &pool() {
   return *p;
 }
 
+hipEvent_t take_event(int device) {
+  {
+    Pool &p = pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    auto &ev = p.devices[device].events;
+    if (!ev.empty()) {
+      hipEvent_t e = ev.back();
+      ev.pop_back();
+      return e;
+    }
+  }
+  hipEvent_t e = nullptr;
+  hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+  return e;
+}
+
+void give_events_locked(Pool &p, int device, const std::vector<Pending> &pend) {
+  auto &ev = p.devices[device].events;
+  for (const Pending &q : pend) ev.push_back(q.event);
+}
+
 // Four size classes per octave, 256 B minimum: at most 25% slack, and a
 // steady-state call sequence maps onto the same few classes.
 size_t round_size(size_t bytes) {
@@ -147,13 +194,14 @@ size_t round_size(size_t bytes) {
 void trim_locked(Pool &p, size_t target) {
   for (auto &dev : p.devices) {
     auto &fb = dev.second.free_blocks;
+    if (p.cached <= target || fb.empty()) continue;
+    DeviceGuard guard(dev.first);
     while (p.cached > target && !fb.empty()) {
       auto it = std::prev(fb.end()); // largest first
-      int cur = 0;
-      (void)hipGetDevice(&cur);
-      (void)hipSetDevice(dev.first);
+      // The block's last users must be done before its memory goes back.
+      for (const Pending &q : it->second.pending) (void)hipEventSynchronize(q.event);
+      give_events_locked(p, dev.first, it->second.pending);
       (void)hipFree(it->second.ptr);
-      (void)hipSetDevice(cur);
       p.cached -= it->second.capacity;
       fb.erase(it);
     }
@@ -162,13 +210,46 @@ void trim_locked(Pool &p, size_t target) {
 
 } // namespace
 
+void Buffer::note_reader(hipStream_t s) {
+  if (s == stream) return;
+  for (hipStream_t r : readers)
+    if (r == s) return;
+  readers.push_back(s);
+}
+
 Buffer::~Buffer() {
   if (!ptr) return;
+  // One event per stream that may still be using the block, recorded now;
+  // retired library streams were synchronised when they were destroyed.
+  std::vector<Pending> pend;
+  {
+    DeviceGuard guard(device);
+    auto record = [&](hipStream_t s) {
+      if (stream_retired(s)) return;
+      hipEvent_t e = nullptr;
+      try {
+        e = take_event(device);
+      } catch (const std::exception &) {
+        (void)hipStreamSynchronize(s); // no event: wait here instead
+        (void)hipGetLastError();
+        return;
+      }
+      if (hipEventRecord(e, s) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(s);
+        (void)hipGetLastError();
+        (void)hipEventDestroy(e);
+        return;
+      }
+      pend.push_back(Pending{e, s});
+    };
+    record(stream);
+    for (hipStream_t r : readers) record(r);
+  }
   Pool &p = pool();
   std::lock_guard<std::mutex> lock(p.mu);
   p.active -= capacity;
-  p.devices[device].free_blocks.emplace(capacity,
-                                        FreeBlock{ptr, capacity, stream});
+  p.devices[device].free_blocks.emplace(capacity, FreeBlock{ptr, capacity, std::move(pend)});
   p.cached += capacity;
   if (p.cached > p.limit) trim_locked(p, p.limit);
 }
@@ -185,18 +266,24 @@ std::shared_ptr<Buffer> allocate(size_t bytes, int device, hipStream_t stream) {
     auto &fb = p.devices[device].free_blocks;
     auto it = fb.lower_bound(want);
     if (it != fb.end() && it->first <= want + want / 4) {
-      FreeBlock blk = it->second;
+      FreeBlock blk = std::move(it->second);
       fb.erase(it);
       p.cached -= blk.capacity;
       p.active += blk.capacity;
       p.peak = std::max(p.peak, p.active);
       lock.unlock();
-      if (blk.stream != stream) {
-        // Last used on another stream: its work must be done before reuse.
-        hip_check(hipStreamSynchronize(blk.stream), "allocator: stream sync");
+      // Work already enqueued on `stream` precedes this use by stream order;
+      // the block's users on other streams are waited for on the device.
+      hipError_t err = hipSuccess;
+      for (const Pending &q : blk.pending)
+        if (q.stream != stream && err == hipSuccess) err = hipStreamWaitEvent(stream, q.event, 0);
+      {
+        std::lock_guard<std::mutex> relock(p.mu);
+        give_events_locked(p, device, blk.pending);
       }
       buf->ptr = blk.ptr;
       buf->capacity = blk.capacity;
+      hip_check(err, "allocator: hipStreamWaitEvent");
       return buf;
     }
   }
@@ -215,6 +302,60 @@ std::shared_ptr<Buffer> allocate(size_t bytes, int device, hipStream_t stream) {
   buf->ptr = ptr;
   buf->capacity = want;
   return buf;
+}
+
+// ---- per-stream workspace ---------------------------------------------------------
+
+namespace {
+
+struct WorkspaceKey {
+  int device;
+  hipStream_t stream;
+  std::thread::id thread; // only for hipStreamPerThread
+  bool operator<(const WorkspaceKey &o) const {
+    if (device != o.device) return device < o.device;
+    if (stream != o.stream) return stream < o.stream;
+    return thread < o.thread;
+  }
+};
+
+struct WorkspaceSlot {
+  std::shared_ptr<Buffer> partial;
+  size_t partial_floats = 0;
+};
+
+std::mutex g_ws_mu;
+std::map<WorkspaceKey, WorkspaceSlot> g_ws;
+
+WorkspaceKey ws_key(int device, hipStream_t stream) {
+  WorkspaceKey k{device, stream, std::thread::id()};
+  if (stream == hipStreamPerThread) k.thread = std::this_thread::get_id();
+  return k;
+}
+
+} // namespace
+
+float *stream_workspace(int device, hipStream_t stream, size_t partial_floats) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  WorkspaceSlot &slot = g_ws[ws_key(device, stream)];
+  if (slot.partial_floats < partial_floats) {
+    // Grows by at least half again, so a growing sequence reallocates rarely;
+    // the old buffer returns to the cache once the stream's work on it is done.
+    const size_t n = std::max(partial_floats, slot.partial_floats + slot.partial_floats / 2);
+    slot.partial = allocate(n * sizeof(float), device, stream);
+    slot.partial_floats = n;
+  }
+  return slot.partial ? static_cast<float *>(slot.partial->ptr) : nullptr;
+}
+
+void release_stream_workspace(int device, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (auto it = g_ws.begin(); it != g_ws.end();) {
+    if (it->first.device == device && it->first.stream == stream)
+      it = g_ws.erase(it);
+    else
+      ++it;
+  }
 }
 
 size_t active_memory() {
@@ -241,6 +382,12 @@ size_t set_cache_limit(size_t limit) {
   return old;
 }
 void clear_cache() {
+  {
+    // Workspaces go back to the cache first (their users are done after the
+    // device synchronisation below).
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    g_ws.clear();
+  }
   std::lock_guard<std::mutex> lock(pool().mu);
   (void)hipDeviceSynchronize();
   trim_locked(pool(), 0);
@@ -252,6 +399,9 @@ namespace {
 
 std::mutex g_stream_mu;
 std::map<int, hipStream_t> g_default_streams;
+// Owned streams destroyed by sdq_stream_free (each synchronised first).  A
+// handle value HIP hands out again for a new stream is taken off the list.
+std::set<hipStream_t> g_retired;
 
 hipStream_t default_stream_for(int device) {
   std::lock_guard<std::mutex> lock(g_stream_mu);
@@ -277,6 +427,11 @@ int current_device() {
 }
 
 } // namespace
+
+bool stream_retired(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_stream_mu);
+  return g_retired.count(s) != 0;
+}
 
 StreamImpl *stream_of(sdq_stream s, const char *op) {
   (void)op;
@@ -572,6 +727,10 @@ sdq_stream sdq_gpu_stream_new(void) {
     hipStream_t h = nullptr;
     hip_check(hipStreamCreateWithFlags(&h, hipStreamNonBlocking),
               "hipStreamCreate");
+    {
+      std::lock_guard<std::mutex> lock(g_stream_mu);
+      g_retired.erase(h);
+    }
     s->stream = h;
     s->owned = true;
     return sdq_stream{s};
@@ -584,7 +743,14 @@ sdq_stream sdq_gpu_stream_new(void) {
 int sdq_stream_free(sdq_stream s) {
   auto *impl = static_cast<StreamImpl *>(s.ctx);
   if (impl && impl->owned && impl->stream) {
+    // Everything enqueued on the stream completes before it goes: blocks and
+    // arrays still tagged with it then need no wait on it (stream_retired).
     (void)hipStreamSynchronize(impl->stream);
+    {
+      std::lock_guard<std::mutex> lock(g_stream_mu);
+      g_retired.insert(impl->stream);
+    }
+    release_stream_workspace(impl->device, impl->stream);
     (void)hipStreamDestroy(impl->stream);
   }
   delete impl;
