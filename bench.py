@@ -1,18 +1,32 @@
 #!/usr/bin/env python3
 """Benchmark of the MLX-affine quantized linear on one MI355X.
 
-Workload (the metric's "Flux 3072->12288" shape): the
-Flux double-block MLP pair on 1536 tokens with bf16 activations --
-fc1 3072->12288 at 4 bits, tanh-GELU, fc2 12288->3072 at 8 bits, group 64,
-f32 scales and biases, weights N(0, 0.02) before quantization.  One step is
-fc1 + GELU + fc2 over the whole batch; inputs are resident in HBM before the
-timed region starts.  The quantized weights rotate through distinct copies
-totalling more than the 256 MB Infinity Cache, so every step streams its
+Headline workload (the metric's "Flux 3072->12288" shape):
+the Flux double-block MLP pair on 1536 tokens with bf16 activations -- fc1
+3072->12288 at 4 bits, tanh-GELU, fc2 12288->3072 at 8 bits, group 64, f32
+scales and biases, weights N(0, 0.02) before quantization.  One step is fc1 +
+GELU + fc2 over the whole batch; inputs are resident in HBM before the timed
+region starts.  The quantized weights rotate through distinct copies totalling
+more than 512 MB (twice the 256 MB Infinity Cache), so every step streams its
 weights from HBM.
+
+Protocol (the reference's: docs/handoff.md:2162-2175, minimum of interleaved
+repetitions): a fixed-duration untimed clock warm-up, then --warmup steps,
+then --reps repetitions that each time exactly --steps steps of the fused form
+(GELU in fc1's epilogue) and then --steps steps of the unfused form (fc1, the
+GELU kernel, fc2: the reference's sequence of calls); each form reports the
+minimum over its repetitions.
+
+Beside the headline: an M sweep of 3072->12288 at 4 and 8 bits, and BASELINE
+config 5 (every distinct linear of one Flux-schnell step at 1024x1024 with its
+per-step call count, under BASELINE's bit policy and under the reference's
+mixed(4), quantized.rs:156-166).  Those points replay a captured HIP graph of
+one launch per rotated weight copy, so the timing holds the kernels only (no
+host launch overhead); each point rotates more than 512 MB of weights.
 
 The line printed on stdout is the JSON record; everything else goes to
 stderr.  Kernels are timed with HIP events recorded on the stream they are
-launched on (torch's current stream, handed to libsdq's raw entry point).
+launched on (handed to libsdq's raw entry points).
 """
 from __future__ import annotations
 
@@ -31,11 +45,41 @@ sys.path.insert(0, str(REPO / "stable-diffusion.rs_amd"))
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # FLOP per byte
+ROTATE_BYTES = 600 << 20    # weight bytes each timed point rotates through (> 512 MB)
 
 M_TOKENS = 1536
 HIDDEN = 3072
 MLP = 12288
 GS = 64
+
+# the distinct quantized linears of one Flux-schnell step at
+# 1024x1024 (4096 image + 512 text tokens, hidden 3072), from
+# sd-models/src/mlx/flux.rs (double_block 333-420, single_block 424-471,
+# embedders 491-502, final layer 580-600).  (name, M, K, N, calls per step,
+# bits under BASELINE's policy -- residual writers at 8 --, bits under the
+# reference's mixed(4) -- 8 only for the modulation, embedder-in and final
+# layers --).
+CONFIG5 = [
+    ("double img_mod.lin + txt_mod.lin", 1, 3072, 18432, 38, 8, 8),
+    ("double img_attn.qkv", 4096, 3072, 9216, 19, 4, 4),
+    ("double txt_attn.qkv", 512, 3072, 9216, 19, 4, 4),
+    ("double img_attn.proj", 4096, 3072, 3072, 19, 8, 4),
+    ("double txt_attn.proj", 512, 3072, 3072, 19, 8, 4),
+    ("double img_mlp.0 (fc1)", 4096, 3072, 12288, 19, 4, 4),
+    ("double txt_mlp.0 (fc1)", 512, 3072, 12288, 19, 4, 4),
+    ("double img_mlp.2 (fc2)", 4096, 12288, 3072, 19, 8, 4),
+    ("double txt_mlp.2 (fc2)", 512, 12288, 3072, 19, 8, 4),
+    ("single modulation.lin", 1, 3072, 9216, 38, 8, 8),
+    ("single linear1", 4608, 3072, 21504, 38, 4, 4),
+    ("single linear2", 4608, 15360, 3072, 38, 8, 4),
+    ("img_in", 4096, 64, 3072, 1, 8, 8),
+    ("txt_in", 512, 4096, 3072, 1, 8, 8),
+    ("time_in.in_layer", 1, 256, 3072, 1, 4, 4),
+    ("vector_in.in_layer", 1, 768, 3072, 1, 4, 4),
+    ("time_in/vector_in.out_layer", 1, 3072, 3072, 2, 4, 4),
+    ("final_layer.adaLN_modulation.1", 1, 3072, 6144, 1, 8, 8),
+    ("final_layer.linear", 4096, 3072, 64, 1, 8, 8),
+]
 
 
 def log(*a):
@@ -46,13 +90,23 @@ def algorithmic_bytes(M, N, K, bits, x_bytes=2, y_bytes=2, s_bytes=4):
     return N * K * bits // 8 + 2 * N * (K // GS) * s_bytes + M * K * x_bytes + M * N * y_bytes
 
 
+def roofline_point(M, N, K, bits, ms):
+    fl = 2.0 * M * N * K
+    by = algorithmic_bytes(M, N, K, bits)
+    tf, gbs = fl / ms / 1e9, by / ms / 1e6
+    bound = "hbm" if fl / by < RIDGE else "mfma"
+    frac = gbs / PEAK_HBM_GBS if bound == "hbm" else tf / PEAK_BF16_TFLOPS
+    return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1), "GB/s": round(gbs, 1), "bound": bound,
+            "frac": round(frac, 4)}
+
+
 TRAFFIC_FILE = REPO / "profiles" / "bench_config2_hbm_traffic.md"
 
 
 def measured_traffic(label):
-    """Calibrated HBM bytes per dispatch of layer `label` ("fc1"/"fc2") from
-    the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary, with the kernel
-    it was measured on; None when the summary is absent."""
+    """Calibrated HBM bytes per call of layer `label` ("fc1"/"fc2") from the
+    committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary, with the kernel it was
+    measured on; None when the summary is absent."""
     if not TRAFFIC_FILE.exists():
         return None, None
     for line in TRAFFIC_FILE.read_text().splitlines():
@@ -62,31 +116,66 @@ def measured_traffic(label):
     return None, None
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    # The GPU's clocks ramp over the first ~100-150 steps (~40 ms) after idle:
-    # per-step time falls from ~340 to ~277 us.  The warmup covers the ramp.
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--rotate", type=int, default=10, help="distinct weight copies (>= 9 exceeds the MALL)")
+    ap.add_argument("--steps", type=int, default=50, help="steps timed per repetition and form")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed steps after the clock warm-up")
+    ap.add_argument("--clock-warmup", type=float, default=1.5,
+                    help="seconds of untimed steps first: the GPU's clocks ramp over ~0.1 s after idle")
+    ap.add_argument("--reps", type=int, default=5, help="interleaved repetitions (minimum reported)")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-config5", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline work")
     ap.add_argument("--unfused", action="store_true",
-                    help="time the step with GELU as its own kernel between the two matmuls (the reference's "
-                         "sequence of calls) instead of fused into fc1's epilogue; the other form is timed "
-                         "and reported beside it either way")
-    ap.add_argument("--no-compare", action="store_true",
-                    help="skip timing the other GELU form (keeps a profiler's trace to one form)")
+                    help="report the unfused form (fc1, GELU kernel, fc2) as the headline")
+    ap.add_argument("--only", choices=["step", "sweep", "config5"], default=None,
+                    help="run one part only (for profiling its kernels)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, run one f32->bf16 copy of 2^27 elements (512 MiB read, "
                          "256 MiB written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
+class Raw:
+    """ctypes access to the raw entry points on torch-owned device memory."""
+
+    def __init__(self, sdq):
+        self.sdq = sdq
+        self.L = sdq.lib()
+
+    def matmul(self, y, x, w, s, b, M, N, K, bits, hs, act=0, s_dtype=None):
+        sdq = self.sdq
+        sdt = sdq.FLOAT32 if s_dtype is None else s_dtype
+        if act:
+            rc = self.L.sdq_quantized_matmul_epilogue_raw(y, sdq.BFLOAT16, x, sdq.BFLOAT16, K, w, s, b, sdt,
+                                                          M, N, K, GS, bits, None, 0, act, hs)
+        else:
+            rc = self.L.sdq_quantized_matmul_raw(y, sdq.BFLOAT16, x, sdq.BFLOAT16, K, w, s, b, sdt,
+                                                 M, N, K, GS, bits, hs)
+        if rc:
+            sdq._check(rc, "quantized_matmul_raw")
+
+    def gelu(self, out, inp, n, hs):
+        rc = self.L.sdq_gelu_approx_raw(out, inp, self.sdq.BFLOAT16, n, hs)
+        if rc:
+            self.sdq._check(rc, "gelu_approx_raw")
+
+
 class Layer:
-    """One quantized linear, with `rotate` distinct device copies."""
+    """One quantized linear (real MLX-affine quantization of N(0, 0.02)
+    weights), with `rotate` distinct device copies."""
 
     def __init__(self, sdq, stream, N, K, bits, seed, rotate):
         rng = np.random.default_rng(seed)
@@ -105,17 +194,62 @@ class Layer:
         return sum(c.resident_bytes() for c in self.copies)
 
 
-def launch(L, layer, copy, y_ptr, x_ptr, M, hstream, sdq, act=0):
-    w, s, b = layer.ptrs[copy % len(layer.ptrs)]
-    if act:
-        rc = L.sdq_quantized_matmul_epilogue_raw(y_ptr, sdq.BFLOAT16, x_ptr, sdq.BFLOAT16, layer.K, w, s, b,
-                                                 sdq.FLOAT32, M, layer.N, layer.K, GS, layer.bits, None, 0,
-                                                 act, hstream)
-    else:
-        rc = L.sdq_quantized_matmul_raw(y_ptr, sdq.BFLOAT16, x_ptr, sdq.BFLOAT16, layer.K, w, s, b,
-                                        sdq.FLOAT32, M, layer.N, layer.K, GS, layer.bits, hstream)
-    if rc:
-        sdq._check(rc, "quantized_matmul")
+class SynthLayer:
+    """Device-generated quantized weights for timing-only points: uniform
+    random codes and scales/biases of the magnitude N(0, 0.02) weights give
+    (the kernels' work does not depend on the values).  Copies rotate through
+    more than ROTATE_BYTES."""
+
+    def __init__(self, torch, dev, N, K, bits, seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        words = N * K * bits // 32
+        per_copy = words * 4 + 2 * N * (K // GS) * 4
+        # Tiny weights (the embedders) would need thousands of copies: they are
+        # capped, and then sit in the caches as they do in a real step.
+        self.rotate = min(64, max(2, -(-ROTATE_BYTES // per_copy)))
+        self.w = torch.randint(-2**31, 2**31 - 1, (self.rotate, words), device=dev, dtype=torch.int32, generator=g)
+        self.s = torch.rand((self.rotate, N * (K // GS)), device=dev, generator=g) * 0.004 + 0.0005
+        self.b = -self.s * (2 ** (bits - 1))
+        self.N, self.K, self.bits = N, K, bits
+        self.ptrs = [(self.w[i].data_ptr(), self.s[i].data_ptr(), self.b[i].data_ptr()) for i in range(self.rotate)]
+
+
+def graph_time(torch, raw, layer, M, x, y, reps=6):
+    """Per-launch ms of `layer` at M rows: a HIP graph of one launch per weight
+    copy, replayed `reps` times; the minimum replay.  y is written row-major
+    [M, N]; the graph's output is checked bit-for-bit against an eager launch
+    of the same (last) copy."""
+    s = torch.cuda.Stream()
+    nrot = len(layer.ptrs)
+    with torch.cuda.stream(s):
+        hs = s.cuda_stream
+        for i in range(2 * nrot):  # warm the stream's workspace and the clocks
+            w, sc, b = layer.ptrs[i % nrot]
+            raw.matmul(y.data_ptr(), x.data_ptr(), w, sc, b, M, layer.N, layer.K, layer.bits, hs)
+    s.synchronize()
+    out = y.view(-1)[:M * layer.N]
+    ref = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(nrot):
+            w, sc, b = layer.ptrs[i]
+            raw.matmul(y.data_ptr(), x.data_ptr(), w, sc, b, M, layer.N, layer.K, layer.bits, s.cuda_stream)
+    best = float("inf")
+    with torch.cuda.stream(s):
+        for r in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+            e1.synchronize()
+            if r > 0:  # the first replay uploads the graph
+                best = min(best, e0.elapsed_time(e1) / nrot)
+    s.synchronize()
+    if not torch.equal(out, ref):
+        raise RuntimeError(f"graph replay of M={M} N={layer.N} K={layer.K} differs from the eager launch")
+    del g
+    return best
 
 
 def cpu_baseline(args, fc1, fc2):
@@ -146,10 +280,11 @@ def cpu_baseline(args, fc1, fc2):
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": (f"{reps} full config-2 steps (x[1536,3072] @ fc1[12288,3072]^T 4-bit + "
-                   f"x[1536,12288] @ fc2[3072,12288]^T 8-bit) with the oracle's OpenMP f32 qmatmul, "
-                   f"{flops_step * reps / 1e9:.0f} GFLOP in {dt:.1f} s; MLX's CPU backend is absent, "
-                   f"this is the CPU restatement"),
+                   f"x[1536,12288] @ fc2[3072,12288]^T 8-bit) with the oracle's OpenMP f32 qmatmul on "
+                   f"{threads} threads of {cpu_model()}, {flops_step * reps / 1e9:.0f} GFLOP in {dt:.1f} s; "
+                   f"MLX's CPU backend is absent, this is the CPU restatement"),
     }
 
 
@@ -164,177 +299,227 @@ def main():
 
     import sdq
 
-    L = sdq.lib()
+    raw = Raw(sdq)
     if sdq.device_count() < 1 or not torch.cuda.is_available():
         log("no GPU visible")
         return 1
     dev = torch.device("cuda:0")
     s = sdq.Stream.gpu()
-    t_setup = time.perf_counter()
-    fc1 = Layer(sdq, s, MLP, HIDDEN, 4, seed=11, rotate=args.rotate)
-    fc2 = Layer(sdq, s, HIDDEN, MLP, 8, seed=12, rotate=args.rotate)
-    log(f"weights: {args.rotate} copies, {(fc1.resident_bytes() + fc2.resident_bytes()) / 2**20:.0f} MiB "
-        f"resident, setup {time.perf_counter() - t_setup:.1f} s")
-
     g = torch.Generator(device=dev)
     g.manual_seed(5)
-    x = torch.randn(M_TOKENS, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
-    h = torch.empty(M_TOKENS, MLP, device=dev, dtype=torch.bfloat16)
-    a = torch.empty_like(h)
-    y = torch.empty(M_TOKENS, HIDDEN, device=dev, dtype=torch.bfloat16)
-    ts = torch.cuda.current_stream()
-    hs = ts.cuda_stream
+    do_step = args.only in (None, "step")
 
-    def step(i, ev=None, fused=not args.unfused):
-        # fused: GELU in fc1's epilogue (sdq_quantized_matmul_epilogue_raw);
-        # unfused: fc1, then the GELU kernel, then fc2 (the reference's
-        # sequence of calls, flux.rs:400-413).
-        if ev:
-            ev[0].record(ts)
-        if fused:
-            launch(L, fc1, i, a.data_ptr(), x.data_ptr(), M_TOKENS, hs, sdq, act=sdq.ACT_GELU_APPROX)
-        else:
-            launch(L, fc1, i, h.data_ptr(), x.data_ptr(), M_TOKENS, hs, sdq)
-        if ev:
-            ev[1].record(ts)
-        if not fused:
-            rc = L.sdq_gelu_approx_raw(a.data_ptr(), h.data_ptr(), sdq.BFLOAT16, h.numel(), hs)
-            if rc:
-                sdq._check(rc, "gelu_approx_raw")
-        if ev:
-            ev[2].record(ts)
-        launch(L, fc2, i, y.data_ptr(), a.data_ptr(), M_TOKENS, hs, sdq)
-        if ev:
-            ev[3].record(ts)
+    # ---- headline: the config-2 MLP pair -------------------------------------------------
+    fc1 = fc2 = None
+    rec_step = {}
+    if do_step:
+        t_setup = time.perf_counter()
+        per_pair = (MLP * HIDDEN // 2 + 2 * MLP * (HIDDEN // GS) * 4) + (HIDDEN * MLP + 2 * HIDDEN * (MLP // GS) * 4)
+        rotate = max(2, -(-ROTATE_BYTES // per_pair))
+        fc1 = Layer(sdq, s, MLP, HIDDEN, 4, seed=11, rotate=rotate)
+        fc2 = Layer(sdq, s, HIDDEN, MLP, 8, seed=12, rotate=rotate)
+        log(f"weights: {rotate} copies, {(fc1.resident_bytes() + fc2.resident_bytes()) / 2**20:.0f} MiB resident, "
+            f"setup {time.perf_counter() - t_setup:.1f} s")
+        x = torch.randn(M_TOKENS, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
+        h = torch.empty(M_TOKENS, MLP, device=dev, dtype=torch.bfloat16)
+        a = torch.empty_like(h)
+        y = torch.empty(M_TOKENS, HIDDEN, device=dev, dtype=torch.bfloat16)
+        ts = torch.cuda.current_stream()
+        hs = ts.cuda_stream
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    # The timed region holds only the steps: per-call events between kernels
-    # would themselves add gaps, so the per-call times come from a second,
-    # separately timed pass below.
-    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e_start.record(ts)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    e_end.record(ts)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        step(args.warmup + args.steps + i, evs[i])
-    torch.cuda.synchronize()
-    # The other form of the step, timed the same way, for comparison.
-    other_ms = float("nan")
-    if not args.no_compare:
+        def step(i, fused, ev=None):
+            # fused: GELU in fc1's epilogue (sdq_quantized_matmul_epilogue_raw);
+            # unfused: fc1, then the GELU kernel, then fc2 (flux.rs:400-413).
+            w1, s1, b1 = fc1.ptrs[i % rotate]
+            w2, s2, b2 = fc2.ptrs[i % rotate]
+            if ev:
+                ev[0].record(ts)
+            if fused:
+                raw.matmul(a.data_ptr(), x.data_ptr(), w1, s1, b1, M_TOKENS, MLP, HIDDEN, 4, hs,
+                           act=sdq.ACT_GELU_APPROX)
+            else:
+                raw.matmul(h.data_ptr(), x.data_ptr(), w1, s1, b1, M_TOKENS, MLP, HIDDEN, 4, hs)
+            if ev:
+                ev[1].record(ts)
+            if not fused:
+                raw.gelu(a.data_ptr(), h.data_ptr(), h.numel(), hs)
+            if ev:
+                ev[2].record(ts)
+            raw.matmul(y.data_ptr(), a.data_ptr(), w2, s2, b2, M_TOKENS, HIDDEN, MLP, 8, hs)
+            if ev:
+                ev[3].record(ts)
+
+        # Clock warm-up for a fixed time, then the requested warmup steps.
+        t0 = time.perf_counter()
+        n_clock = 0
+        while time.perf_counter() - t0 < args.clock_warmup:
+            for _ in range(20):
+                step(n_clock, fused=not args.unfused)
+                n_clock += 1
+            torch.cuda.synchronize()
         for i in range(args.warmup):
-            step(i, fused=args.unfused)
-        o_start, o_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            step(i, fused=not args.unfused)
         torch.cuda.synchronize()
-        o_start.record(ts)
-        for i in range(args.steps):
-            step(args.warmup + i, fused=args.unfused)
-        o_end.record(ts)
-        torch.cuda.synchronize()
-        other_ms = o_start.elapsed_time(o_end) / args.steps
-    if args.copy_probe:
-        src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
-        dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-    total_ms = e_start.elapsed_time(e_end)
-    ms_step = total_ms / args.steps
-    k_fc1 = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    k_gelu = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
-    k_fc2 = float(np.mean([e[2].elapsed_time(e[3]) for e in evs]))
-    flops_fc1 = 2.0 * M_TOKENS * HIDDEN * MLP
-    flops_fc2 = 2.0 * M_TOKENS * MLP * HIDDEN
-    flops_step = flops_fc1 + flops_fc2
-    value = flops_step / (ms_step / 1e3) / 1e12
-    form, other_form = ("unfused", "fused") if args.unfused else ("fused", "unfused")
-    log(f"step {ms_step:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms, GELU {form}): fc1 {k_fc1:.3f} ms "
-        f"({flops_fc1 / k_fc1 / 1e9:.0f} TFLOP/s), gelu {k_gelu:.3f} ms, fc2 {k_fc2:.3f} ms "
-        f"({flops_fc2 / k_fc2 / 1e9:.0f} TFLOP/s); {other_form} step {other_ms:.3f} ms")
 
-    # Dominant kernel's roofline (MFMA-bound at M = 1536: AI far above the ridge).
-    # One call is the tile kernel plus, when the plan splits K, the reduction
-    # kernel of its partial tiles; the events bracket the whole call.
-    if k_fc1 >= k_fc2:
-        epi = "" if args.unfused else ", GELU epilogue"
-        dom, dom_ms, dom_flops, dom_layer, label = (f"qmm fc1 4-bit 1536x3072->12288 (qmm_kernel + qmm_reduce_kernel{epi})",
-                                                    k_fc1, flops_fc1, fc1, "fc1")
-    else:
-        dom, dom_ms, dom_flops, dom_layer, label = ("qmm fc2 8-bit 1536x12288->3072 (qmm_kernel + qmm_reduce_kernel)",
-                                                    k_fc2, flops_fc2, fc2, "fc2")
-    achieved = dom_flops / (dom_ms / 1e3) / 1e12
-    traffic, traffic_kernel = measured_traffic(label)
-    roofline = {
-        "kernel": dom,
-        "bound": "mfma",
-        "achieved": round(achieved, 2),
-        "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": traffic,
-        "traffic_source": (f"{TRAFFIC_FILE.relative_to(REPO)} ({traffic_kernel}, rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                           "copy-calibrated)") if traffic else None,
-        "flops_per_launch": dom_flops,
-        "algorithmic_bytes_per_launch": algorithmic_bytes(M_TOKENS, dom_layer.N, dom_layer.K, dom_layer.bits),
-        "avg_launch_ms": round(dom_ms, 4),
-    }
-
-    sweep = []
-    if not args.no_sweep:
-        fc1_8 = Layer(sdq, s, MLP, HIDDEN, 8, seed=13, rotate=args.rotate)
-        xs = torch.randn(4608, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
-        ys = torch.empty(4608, MLP, device=dev, dtype=torch.bfloat16)
-        for bits, layer in ((4, fc1), (8, fc1_8)):
-            for M in (1, 4, 16, 32, 64, 256, 1024, 1536, 4608):
-                reps = 30 if M <= 64 else 10
-                for i in range(3):
-                    launch(L, layer, i, ys.data_ptr(), xs.data_ptr(), M, hs, sdq)
+        # Interleaved repetitions: each times exactly --steps steps of each form.
+        times = {True: [], False: []}
+        t_wall = time.perf_counter()
+        for r in range(args.reps):
+            for fused in (True, False):
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 torch.cuda.synchronize()
                 e0.record(ts)
-                for i in range(reps):
-                    launch(L, layer, i, ys.data_ptr(), xs.data_ptr(), M, hs, sdq)
+                for i in range(args.steps):
+                    step(i, fused)
                 e1.record(ts)
                 torch.cuda.synchronize()
-                ms = e0.elapsed_time(e1) / reps
-                fl = 2.0 * M * MLP * HIDDEN
-                by = algorithmic_bytes(M, MLP, HIDDEN, bits)
-                tf, gbs = fl / ms / 1e9, by / ms / 1e6
-                bound = "hbm" if fl / by < RIDGE else "mfma"
-                frac = gbs / PEAK_HBM_GBS if bound == "hbm" else tf / PEAK_BF16_TFLOPS
-                sweep.append({"M": M, "bits": bits, "us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
-                              "GB/s": round(gbs, 1), "bound": bound, "frac": round(frac, 4)})
-                log(f"sweep 3072->12288 {bits}-bit M={M:5d}: {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s "
-                    f"{gbs:8.1f} GB/s  {bound} {frac * 100:5.1f}%")
-        del fc1_8
+                times[fused].append(e0.elapsed_time(e1) / args.steps)
+        wall = time.perf_counter() - t_wall
+        head_fused = not args.unfused
+        ms_step = min(times[head_fused])
+        other_ms = min(times[not head_fused])
+        # Per-call times: a separate pass with events around each call (events
+        # between kernels add gaps, so they are not in the timed region above).
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+        for i in range(args.steps):
+            step(i, head_fused, evs[i])
+        torch.cuda.synchronize()
+        if args.copy_probe:
+            src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
+            dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+        k_fc1 = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
+        k_gelu = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
+        k_fc2 = float(np.median([e[2].elapsed_time(e[3]) for e in evs]))
+        flops_fc1 = 2.0 * M_TOKENS * HIDDEN * MLP
+        flops_fc2 = 2.0 * M_TOKENS * MLP * HIDDEN
+        form, other_form = ("fused", "unfused") if head_fused else ("unfused", "fused")
+        log(f"step {ms_step:.4f} ms ({form}; reps {', '.join(f'{t:.4f}' for t in times[head_fused])}), "
+            f"{other_form} {other_ms:.4f} ms; per call: fc1 {k_fc1:.4f} ms, gelu {k_gelu:.4f} ms, "
+            f"fc2 {k_fc2:.4f} ms; clock warm-up {n_clock} steps; timed wall {wall:.2f} s")
+        # Dominant kernel's roofline (MFMA-bound at M = 1536: AI far above the
+        # ridge).  A call is the tile kernel plus, when the plan splits K, the
+        # reduction kernel of its partial tiles; the events bracket the call.
+        if k_fc1 >= k_fc2:
+            epi = ", GELU epilogue" if head_fused else ""
+            dom, dom_ms, dom_flops, dom_layer, label = (
+                f"qmm fc1 4-bit 1536x3072->12288 (qmm_kernel + qmm_reduce_kernel{epi})", k_fc1, flops_fc1, fc1, "fc1")
+        else:
+            dom, dom_ms, dom_flops, dom_layer, label = (
+                "qmm fc2 8-bit 1536x12288->3072 (qmm_kernel + qmm_reduce_kernel)", k_fc2, flops_fc2, fc2, "fc2")
+        achieved = dom_flops / (dom_ms / 1e3) / 1e12
+        traffic, traffic_kernel = measured_traffic(label)
+        rec_step = {
+            "ms_per_step": round(ms_step, 4),
+            f"ms_per_step_{other_form}": round(other_ms, 4),
+            "value": round((flops_fc1 + flops_fc2) / (ms_step / 1e3) / 1e12, 2),
+            "kernels_ms": {"fc1": round(k_fc1, 4), "gelu": round(k_gelu, 4), "fc2": round(k_fc2, 4)},
+            "protocol": {"clock_warmup_s": args.clock_warmup, "clock_warmup_steps": n_clock,
+                         "warmup_steps": args.warmup, "reps": args.reps, "steps_per_rep": args.steps,
+                         "reported": "minimum over interleaved repetitions (fused, unfused alternating)",
+                         "weight_copies_rotated": rotate,
+                         "rotated_mib": round((fc1.resident_bytes() + fc2.resident_bytes()) / 2**20)},
+            "roofline": {
+                "kernel": dom,
+                "bound": "mfma",
+                "achieved": round(achieved, 2),
+                "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic,
+                "traffic_source": (f"{TRAFFIC_FILE.relative_to(REPO)} ({traffic_kernel}, rocprofv3 FETCH_SIZE + "
+                                   "WRITE_SIZE, copy-calibrated)") if traffic else None,
+                "flops_per_launch": dom_flops,
+                "algorithmic_bytes_per_launch": algorithmic_bytes(M_TOKENS, dom_layer.N, dom_layer.K, dom_layer.bits),
+                "avg_launch_ms": round(dom_ms, 4),
+            },
+        }
+        del h, a, y
+
+    # ---- M sweep of 3072->12288 ---------------------------------------------------------------
+    sweep = []
+    if args.only in (None, "sweep") and not args.no_sweep:
+        xs = torch.randn(4608, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
+        ys = torch.empty(4608, MLP, device=dev, dtype=torch.bfloat16)
+        for bits in (4, 8):
+            layer = SynthLayer(torch, dev, MLP, HIDDEN, bits, seed=20 + bits)
+            for M in (1, 4, 16, 32, 64, 128, 256, 512, 1024, 1536, 4608):
+                ms = graph_time(torch, raw, layer, M, xs, ys)
+                pt = {"M": M, "bits": bits, **roofline_point(M, MLP, HIDDEN, bits, ms), "copies": layer.rotate}
+                sweep.append(pt)
+                log(f"sweep 3072->12288 {bits}-bit M={M:5d}: {pt['us']:9.2f} us {pt['TFLOP/s']:8.1f} TFLOP/s "
+                    f"{pt['GB/s']:8.1f} GB/s  {pt['bound']} {pt['frac'] * 100:5.1f}%  ({layer.rotate} copies)")
+            del layer
+        del xs, ys
+
+    # ---- config 5: one Flux-schnell step's quantized linears ------------------------------------
+    config5 = None
+    if args.only in (None, "config5") and not args.no_config5:
+        xs = torch.randn(4608 * 15360, device=dev, generator=g).to(torch.bfloat16)
+        ys = torch.empty(4608 * 21504, device=dev, dtype=torch.bfloat16)
+        shapes = {}
+        for name, M, K, N, calls, b_bl, b_ref in CONFIG5:
+            for bits in {b_bl, b_ref}:
+                key = (M, K, N, bits)
+                if key in shapes:
+                    continue
+                layer = SynthLayer(torch, dev, N, K, bits, seed=M + K + N + bits)
+                ms = graph_time(torch, raw, layer, M, xs, ys)
+                shapes[key] = ms
+                del layer
+        flops_step = 0.0
+        per_policy = {}
+        for policy, idx in (("baseline", 5), ("reference_mixed4", 6)):
+            rows, total_ms = [], 0.0
+            for entry in CONFIG5:
+                name, M, K, N, calls = entry[:5]
+                bits = entry[idx]
+                ms = shapes[(M, K, N, bits)]
+                total_ms += calls * ms
+                if policy == "baseline":
+                    flops_step += calls * 2.0 * M * N * K
+                rows.append({"linear": name, "M": M, "K": K, "N": N, "bits": bits, "calls": calls,
+                             "ms_total": round(calls * ms, 4), **roofline_point(M, N, K, bits, ms)})
+            per_policy[policy] = {"ms_per_step": round(total_ms, 3), "shapes": rows}
+        for policy, v in per_policy.items():
+            v["TFLOP/s"] = round(flops_step / (v["ms_per_step"] / 1e3) / 1e12, 1)
+            v["mfma_frac"] = round(v["TFLOP/s"] / PEAK_BF16_TFLOPS, 4)
+            log(f"config5 [{policy}]: {v['ms_per_step']:.3f} ms of quantized matmul per step, "
+                f"{v['TFLOP/s']:.0f} TFLOP/s ({v['mfma_frac'] * 100:.1f}% of MFMA peak)")
+            for r in v["shapes"]:
+                log(f"    {r['linear']:34s} {r['M']:5d}x{r['K']:5d}->{r['N']:5d} {r['bits']}-bit x{r['calls']:2d}: "
+                    f"{r['us']:8.2f} us/call  {r['bound']} {r['frac'] * 100:5.1f}%")
+        config5 = {"tflop_per_step": round(flops_step / 1e12, 3),
+                   "note": "summed quantized-matmul time of one Flux-schnell step at 1024x1024 (graph replays "
+                           "per distinct shape, times its per-step call count); baseline = BASELINE's bits "
+                           "(residual writers 8-bit), reference_mixed4 = quantized.rs:156-166",
+                   **per_policy}
+        del xs, ys
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if do_step and not args.no_cpu_baseline:
         t = time.perf_counter()
         cpu = cpu_baseline(args, fc1, fc2)
-        log(f"cpu baseline {cpu['value'] * 1e3:.2f} GFLOP/s on {cpu['cores']} threads ({time.perf_counter() - t:.1f} s)")
+        log(f"cpu baseline {cpu['value'] * 1e3:.2f} GFLOP/s on {cpu['cores']} threads of {cpu['cpu_model']} "
+            f"({time.perf_counter() - t:.1f} s)")
 
     rec = {
         "metric": "quantized-matmul TFLOP/s + HBM GB/s (% roofline), Flux 3072->12288, 4/8-bit, M=1..4608",
-        "value": round(value, 2),
+        "value": rec_step.get("value"),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "ms_per_step": rec_step.get("ms_per_step"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: weights N(0,0.02) f32 quantized MLX-affine group 64; activations N(0,1) bf16",
+        "data": "synthetic: weights N(0,0.02) f32 quantized MLX-affine group 64 (headline); sweep and config-5 "
+                "points use device-random codes and scales of the same magnitude; activations N(0,1) bf16",
         "config": {
             "workload": "BASELINE config 2: Flux double-block MLP pair, 1536 tokens (512x512): "
                         "fc1 3072->12288 4-bit, tanh-GELU, fc2 12288->3072 8-bit, group 64, "
@@ -342,15 +527,13 @@ def main():
             "global_batch": M_TOKENS,
             "seq_len": M_TOKENS,
             "parallelism": "single GPU",
-            "weight_copies_rotated": args.rotate,
             "gelu": "separate kernel between the matmuls (sdq_gelu_approx_raw)" if args.unfused else
                     "fused into fc1's epilogue (sdq_quantized_matmul_epilogue_raw)",
         },
-        f"ms_per_step_{other_form}": None if args.no_compare else round(other_ms, 4),
-        "kernels_ms": {"fc1": round(k_fc1, 4), "gelu": round(k_gelu, 4), "fc2": round(k_fc2, 4)},
-        "roofline": roofline,
+        **{k: v for k, v in rec_step.items() if k not in ("value", "ms_per_step")},
         "cpu_baseline": cpu,
         "sweep_3072x12288": sweep,
+        "config5": config5,
     }
     print(json.dumps(rec), flush=True)
     return 0
