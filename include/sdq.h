@@ -301,6 +301,25 @@ int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x,
                                       const void *bias, int bias_dtype,
                                       int activation, void *hip_stream);
 
+/* sdq_quantized_matmul_epilogue_raw for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  It has no counterpart in the reference (MLX allocates
+ * its own scratch).  Same arguments, validation and results to the north
+ * star's tolerance; it calls no hipMalloc, hipFree or allocating library
+ * routine.  The large-M kernel's split-K partial tiles live in a fixed
+ * 16 MiB scratch array per GPU, held until the process ends; the launch
+ * planner takes no split that would need more (so the summation order, and
+ * the last bits of the result, may differ from the allocating entry point's
+ * for some shapes).  All calls on one GPU share that array: calls that
+ * overlap on one GPU (on different streams, or from several threads) race;
+ * calls ordered on one stream do not. */
+int sdq_quantized_matmul_noalloc(void *y, int y_dtype, const void *x, int x_dtype,
+                                 int64_t ldx, const uint32_t *w, const void *scales,
+                                 const void *biases, int s_dtype, int64_t M,
+                                 int64_t N, int64_t K, int group_size, int bits,
+                                 const void *bias, int bias_dtype, int activation,
+                                 void *hip_stream);
+
 /* tanh-GELU on caller-owned device memory (dtype float32/bfloat16/float16),
  * enqueued on `hip_stream`: the elementwise step between the two Flux MLP
  * linears (flux.rs:400-413) without an array handle. */

@@ -59,6 +59,7 @@ def _combo_flags(c):
 SOURCES = [
     (CSRC / "sdq_runtime.cpp", [], None),
     (CSRC / "sdq_ops.cpp", [], None),
+    (CSRC / "sdq_noalloc.hip", [], None),
     (CSRC / "kernels" / "quant.hip", ["-ffp-contract=off"], None),
     (CSRC / "kernels" / "elementwise.hip", [], None),
     (CSRC / "kernels" / "dense.hip", [], None),

@@ -103,7 +103,11 @@ struct QmmPlan {
 };
 
 // y [M, N] = x [M, K] @ dequantize(w).T for any M.  qmm.hip.
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus);
+// max_partial_floats caps the split-K workspace the plan may use (the
+// no-allocation entry point's fixed scratch); a split that would need more
+// is not taken.
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus,
+                 size_t max_partial_floats = ~size_t(0));
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,

@@ -38,7 +38,7 @@ namespace {
 
 namespace kern {
 
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_floats) {
   QmmPlan p;
   p.bm = M <= 128 ? 128 : 256;
   p.tiles_n = int((N + qmm_detail::kTileN - 1) / qmm_detail::kTileN);
@@ -64,6 +64,7 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus) {
       const int64_t sps = (steps + s - 1) / s;
       if (sps < 2) break;
       const int64_t ranges = (steps + sps - 1) / sps;
+      if (size_t(rem * ranges) * size_t(p.bm) * qmm_detail::kTileN > max_partial_floats) continue;
       const int64_t cost = sps * 1000 + kSplitFixed + rem * ranges * kReducePerRange;
       if (cost < best) {
         best = cost;

@@ -77,6 +77,9 @@ void clear_cache();
 float *stream_workspace(int device, hipStream_t stream, size_t partial_floats);
 void release_stream_workspace(int device, hipStream_t stream);
 
+// Compute units of a device (cached).
+int cu_count(int device);
+
 // ---- streams ------------------------------------------------------------
 
 struct StreamImpl {

@@ -52,19 +52,6 @@ void check_group_bits(int gs, int bits) {
          " is not supported. The supported bits are 2, 4 and 8.");
 }
 
-int cu_count(int device) {
-  static std::mutex mu;
-  static std::map<int, int> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(device);
-  if (it != cache.end()) return it->second;
-  int n = 0;
-  hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device),
-            "hipDeviceGetAttribute");
-  cache[device] = n;
-  return n;
-}
-
 // y = x @ dequantize(w).T on device pointers; picks the kernel by M.
 void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
                      const uint32_t *w, const void *scales, const void *biases,
@@ -97,6 +84,20 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
 }
 
 } // namespace
+
+int cu_count(int device) {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(device);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device),
+            "hipDeviceGetAttribute");
+  cache[device] = n;
+  return n;
+}
+
 } // namespace sdq
 
 using namespace sdq;

@@ -187,6 +187,11 @@ def _declare(L: ctypes.CDLL) -> None:
             [c_vp, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
              ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
         ),
+        "sdq_quantized_matmul_noalloc": (
+            c_int,
+            [c_vp, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
+             ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
+        ),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
         "sdq_array_device_ptr": (c_vp, [A]),
         "sdq_version": (ctypes.c_char_p, []),
