@@ -274,6 +274,44 @@ int sdq_gelu_approx(sdq_array *res, sdq_array a, sdq_stream s);
  * b: [N, K]; result [..., N]. */
 int sdq_matmul_nt(sdq_array *res, sdq_array a, sdq_array b, sdq_stream s);
 
+/* ---- GGUF tensors: the quantized loader ------------------------------------ */
+
+/* GGML type ids as a GGUF file writes them (mlx_gguf.rs:61-79). */
+typedef enum sdq_ggml_type_ {
+  SDQ_GGML_F32 = 0,
+  SDQ_GGML_F16 = 1,
+  SDQ_GGML_Q4_0 = 2,  /* 32 values: f16 d, 16 nibble bytes */
+  SDQ_GGML_Q8_0 = 8,  /* 32 values: f16 d, 32 signed bytes */
+  SDQ_GGML_Q4_K = 12, /* 256 values in 144 bytes */
+  SDQ_GGML_Q5_K = 13, /* 256 values in 176 bytes */
+  SDQ_GGML_Q6_K = 14, /* 256 values in 210 bytes */
+  SDQ_GGML_BF16 = 30
+} sdq_ggml_type;
+
+/* replaces Gguf::dequantize (mlx_gguf.rs:235-276) followed by
+ * Array::from_slice_f32 (quantized.rs:190-191): the block decoding runs on
+ * the device.  raw: a uint8 array holding the tensor's bytes exactly as the
+ * file stores them (the caller reads them at data_start + offset, as
+ * mlx_gguf.rs:246-250 does); shape: the tensor's row-major shape (the file's
+ * dimensions reversed, mlx_gguf.rs:97-104, 208).  res: float32 [shape], the
+ * values of mlx_gguf.rs's decoders bit for bit.  Fails, naming the type, for
+ * a type outside the set above, and when the element count is not a multiple
+ * of the block size or the byte count does not match the shape. */
+int sdq_gguf_dequantize(sdq_array *res, sdq_array raw, int ggml_type,
+                        const int *shape, int ndim, sdq_stream s);
+
+/* replaces the loader's sequence Gguf::dequantize -> Array::from_slice_f32
+ * -> QuantizedArray::quantize (quantized.rs:190-196, 236-243): one kernel
+ * decodes the blocks and quantizes the f32 values to the MLX-affine layout,
+ * so the dense tensor is never written.  res: three arrays as sdq_quantize
+ * returns them for a float32 matrix -- packed [..., K*bits/32] uint32, f32
+ * scales and biases [..., K/group_size] -- equal to sdq_quantize of
+ * sdq_gguf_dequantize's result.  Shape rules as sdq_quantize, type and size
+ * rules as sdq_gguf_dequantize. */
+int sdq_gguf_quantize(sdq_vector_array *res, sdq_array raw, int ggml_type,
+                      const int *shape, int ndim, sdq_optional_int group_size,
+                      sdq_optional_int bits, sdq_stream s);
+
 /* ---- raw-pointer entry point ------------------------------------------------- */
 
 /* The kernel behind sdq_quantized_matmul on caller-owned device memory:

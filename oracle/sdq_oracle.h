@@ -14,6 +14,8 @@
  *       MLX's CPU backend, which is not vendored; restated below)
  *   - QuantizedArray::resident_bytes   crates/sd-tensor/src/mlx.rs:1977-1985
  *   - Array::gelu_approx               crates/sd-tensor/src/mlx.rs:1041-1054
+ *   - GGUF block decoders (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)
+ *       crates/sd-tensor/src/mlx_gguf.rs:27-438 (sdq_oracle_gguf.c)
  *
  * Pinning status of each function is recorded beside it and in the tests
  * (tests/test_oracle.py).  Every function here is checked there against
@@ -93,6 +95,21 @@ uint64_t sdo_resident_bytes(int64_t rows, int64_t cols, int group_size,
 /* 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))) evaluated op by op in f32 in the
  * order of mlx.rs:1048-1053. */
 void sdo_gelu_approx(const float *x, float *y, size_t n);
+
+/* ---- GGUF block decoding (sdq_oracle_gguf.c; mlx_gguf.rs:27-438) -------- */
+/* GGML type ids as written in a GGUF file (mlx_gguf.rs:61-79). */
+enum {
+  SDO_GGML_F32 = 0, SDO_GGML_F16 = 1, SDO_GGML_Q4_0 = 2, SDO_GGML_Q8_0 = 8,
+  SDO_GGML_Q4_K = 12, SDO_GGML_Q5_K = 13, SDO_GGML_Q6_K = 14, SDO_GGML_BF16 = 30
+};
+/* (values per block, bytes per block) of a type; -1 for an unsupported id. */
+int sdo_gguf_block(int type, int64_t *values, int64_t *bytes);
+/* The reference's f16 decoder (mlx_gguf.rs:302-318), in its arithmetic form. */
+float sdo_gguf_f16(uint16_t h);
+/* Decodes n values of `type` from raw (exactly n/values*bytes bytes) into
+ * out, as Gguf::dequantize does (mlx_gguf.rs:235-276).  Returns 0, or -1 on
+ * an unsupported type or a size mismatch. */
+int sdo_gguf_dequantize(const uint8_t *raw, size_t raw_bytes, int type, int64_t n, float *out);
 
 #ifdef __cplusplus
 }

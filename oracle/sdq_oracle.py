@@ -54,6 +54,12 @@ def lib() -> ctypes.CDLL:
         L.sdo_resident_bytes.argtypes = [i64, i64, c_int, c_int]
         L.sdo_gelu_approx.restype = None
         L.sdo_gelu_approx.argtypes = [vp, vp, ctypes.c_size_t]
+        L.sdo_gguf_block.restype = c_int
+        L.sdo_gguf_block.argtypes = [c_int, ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        L.sdo_gguf_f16.restype = ctypes.c_float
+        L.sdo_gguf_f16.argtypes = [ctypes.c_uint16]
+        L.sdo_gguf_dequantize.restype = c_int
+        L.sdo_gguf_dequantize.argtypes = [vp, ctypes.c_size_t, c_int, i64, vp]
         for n in ("sdo_bf16_from_f32", "sdo_f16_from_f32"):
             getattr(L, n).restype = ctypes.c_uint16
             getattr(L, n).argtypes = [ctypes.c_float]
@@ -185,3 +191,31 @@ def f16_from_f32(v: float) -> int:
 
 def f32_from_f16(h: int) -> float:
     return lib().sdo_f32_from_f16(h)
+
+
+# ---- GGUF block decoding (sdq_oracle_gguf.c; mlx_gguf.rs:27-438) ----------
+
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
+GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_BF16 = 12, 13, 14, 30
+
+
+def gguf_block(ggml_type: int) -> tuple[int, int]:
+    """(values per block, bytes per block) of a GGML type."""
+    v, b = ctypes.c_int64(), ctypes.c_int64()
+    if lib().sdo_gguf_block(ggml_type, ctypes.byref(v), ctypes.byref(b)) != 0:
+        raise ValueError(f"oracle: GGML type {ggml_type} is not supported")
+    return v.value, b.value
+
+
+def gguf_f16(h: int) -> float:
+    return lib().sdo_gguf_f16(h)
+
+
+def gguf_dequantize(raw, ggml_type: int, n: int) -> np.ndarray:
+    """Decodes n values of a GGML tensor's raw bytes to f32 (Gguf::dequantize)."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(raw), dtype=np.uint8) if not isinstance(raw, np.ndarray) else raw,
+                               dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().sdo_gguf_dequantize(_p(raw), raw.size, ggml_type, n, _p(out)) != 0:
+        raise ValueError("oracle gguf_dequantize rejected its arguments")
+    return out

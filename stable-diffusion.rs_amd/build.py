@@ -52,15 +52,16 @@ def _combo_flags(c):
     return [f"-DSDQ_XD={c[0]}", f"-DSDQ_SD={c[1]}", f"-DSDQ_OD={c[2]}"]
 
 
-# Sources, their extra flags and object names.  quant.hip must round every
-# operation once (bit-exact quantize/dequantize), so contraction into FMA is
-# off there.  The matmul kernels' instantiation units are compiled once per
+# Sources, their extra flags and object names.  quant.hip and gguf.hip must
+# round every operation once (bit-exact quantize/dequantize and GGUF
+# decoding), so contraction into FMA is off there.  The matmul kernels' instantiation units are compiled once per
 # dtype combination.
 SOURCES = [
     (CSRC / "sdq_runtime.cpp", [], None),
     (CSRC / "sdq_ops.cpp", [], None),
     (CSRC / "sdq_noalloc.hip", [], None),
     (CSRC / "kernels" / "quant.hip", ["-ffp-contract=off"], None),
+    (CSRC / "kernels" / "gguf.hip", ["-ffp-contract=off"], None),
     (CSRC / "kernels" / "elementwise.hip", [], None),
     (CSRC / "kernels" / "dense.hip", [], None),
     (CSRC / "kernels" / "qmv.hip", [], None),

@@ -23,6 +23,19 @@ void dequantize(const uint32_t *wq, const void *scales, const void *biases,
                 int s_dtype, int64_t rows, int64_t cols, int group_size,
                 int bits, void *out, int out_dtype, hipStream_t stream);
 
+// GGUF tensors (gguf.hip).  `raw` holds the tensor's GGML blocks as the file
+// stores them (16-byte aligned, raw_bytes = n / values * bytes).
+// (values, bytes) per block of GGML type `type`; false if unsupported.
+bool gguf_block(int type, int64_t *values, int64_t *bytes);
+// out[0..n) = the decoded f32 values (mlx_gguf.rs:235-276).
+void gguf_dequantize(const uint8_t *raw, int type, int64_t n, int64_t raw_bytes, float *out,
+                     hipStream_t stream);
+// The decoded [rows, cols] tensor quantized as quantize() would quantize its
+// f32 values: wq [rows, cols*bits/32], f32 scales/biases [rows, cols/group_size].
+void gguf_quantize(const uint8_t *raw, int type, int64_t rows, int64_t cols, int64_t raw_bytes,
+                   int group_size, int bits, uint32_t *wq, float *scales, float *biases,
+                   hipStream_t stream);
+
 // Output epilogue of the matmul kernels, applied to each f32 result before
 // the output's rounding:
 //   v = act(acc + bias[n])                      (bias optional, act 0 or GELU)

@@ -16,6 +16,7 @@
 //   dequantize: w = round_T(round_T(q * scale) + bias), T = the scales' dtype.
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "quant_group.hpp"
 
 #include "../sdq_internal.hpp"
 
@@ -25,14 +26,6 @@ namespace {
 using namespace dev;
 
 constexpr int kThreads = 256;
-
-// Elements handled by one thread: one word at 2 bits, two words at 8 bits,
-// one word at 4 bits.  A group's threads are consecutive lanes of one wave.
-template <int BITS> struct QuantShape {
-  static constexpr int kPerThread = BITS == 2 ? 16 : 8;
-  static constexpr int kPerWord = 32 / BITS;
-  static constexpr int kWords = kPerThread / kPerWord;
-};
 
 template <int WDT, int N> __device__ __forceinline__ void load_elems(const typename Elem<WDT>::T *p, float (&v)[N]) {
   if constexpr (WDT == SDQ_FLOAT32) {
@@ -64,56 +57,17 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
     typename Elem<WDT>::T *__restrict__ biases) {
   using Shape = QuantShape<BITS>;
   constexpr int C = Shape::kPerThread;
-  constexpr int T = GS / C; // threads per group, a power of two <= 16
-  const float n_bins = float((1 << BITS) - 1);
-  const float eps = 1e-7f;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   for (int64_t c = int64_t(blockIdx.x) * kThreads + threadIdx.x; c < n_chunks;
        c += stride) {
-    // n_chunks is a multiple of T and T divides the wave, so the T lanes of a
-    // group are either all in range here or all out of it.
+    // n_chunks is a multiple of the lanes per group, which divides the wave,
+    // so the lanes of a group are either all in range here or all out of it.
     float v[C];
     load_elems<WDT, C>(w + c * C, v);
-    float lo = v[0], hi = v[0];
-#pragma unroll
-    for (int e = 1; e < C; ++e) {
-      lo = fminf(lo, v[e]);
-      hi = fmaxf(hi, v[e]);
-    }
-#pragma unroll
-    for (int off = T / 2; off > 0; off >>= 1) {
-      lo = fminf(lo, __shfl_xor(lo, off));
-      hi = fmaxf(hi, __shfl_xor(hi, off));
-    }
-    const bool neg_edge = fabsf(lo) > fabsf(hi);
-    float scale = (hi - lo) / n_bins;
-    scale = scale < eps ? eps : scale;
-    scale = neg_edge ? scale : -scale;
-    const float edge = neg_edge ? lo : hi;
-    const float q0 = rintf(edge / scale);
-    float bias = 0.0f;
-    if (q0 != 0.0f) {
-      scale = edge / q0;
-      bias = edge;
-    }
     uint32_t words[Shape::kWords];
-#pragma unroll
-    for (int i = 0; i < Shape::kWords; ++i) words[i] = 0u;
-#pragma unroll
-    for (int e = 0; e < C; ++e) {
-      float q = rintf((v[e] - bias) / scale);
-      q = fminf(fmaxf(q, 0.0f), n_bins);
-      words[e / Shape::kPerWord] |= uint32_t(q) << ((e % Shape::kPerWord) * BITS);
-    }
-    if constexpr (Shape::kWords == 2) {
-      *reinterpret_cast<u32x2 *>(wq + c * 2) = u32x2{words[0], words[1]};
-    } else {
-      wq[c] = words[0];
-    }
-    if ((c & (T - 1)) == 0) {
-      scales[c / T] = Elem<WDT>::store(scale);
-      biases[c / T] = Elem<WDT>::store(bias);
-    }
+    float scale, bias;
+    quantize_group<BITS, GS>(v, words, scale, bias);
+    store_group<BITS, GS, WDT>(c, words, scale, bias, wq, scales, biases);
   }
 }
 

@@ -530,3 +530,100 @@ int sdq_gelu_approx(sdq_array *res, sdq_array a, sdq_stream s) {
 }
 
 } // extern "C"
+
+// ---- GGUF tensors (mlx_gguf.rs:235-276; quantized.rs:181-258) ----------------
+
+namespace {
+
+// The shape of a GGUF tensor as the caller read it from the file's directory
+// (already row-major, mlx_gguf.rs:97-104, 208), checked against its raw bytes.
+struct GgufTensor {
+  std::vector<int> shape;
+  int64_t n = 1;
+  int64_t raw_bytes = 0;
+};
+
+GgufTensor gguf_tensor(const ArrayImpl *raw, int ggml_type, const int *shape, int ndim) {
+  int64_t per = 0, bytes = 0;
+  if (!kern::gguf_block(ggml_type, &per, &bytes))
+    fail("gguf: type " + std::to_string(ggml_type) +
+         " is not one this project's checkpoints use; the supported set is F32, F16, BF16, "
+         "Q4_0, Q8_0, Q4_K, Q5_K, Q6_K");
+  if (raw->dtype != SDQ_UINT8) fail("gguf: `raw` must be a uint8 array of the tensor's bytes");
+  if (ndim < 0 || (ndim > 0 && !shape)) fail("gguf: invalid shape");
+  GgufTensor t;
+  for (int i = 0; i < ndim; ++i) {
+    if (shape[i] < 0) fail("gguf: negative dimension in shape " + shape_str(std::vector<int>(shape, shape + ndim)));
+    t.shape.push_back(shape[i]);
+    t.n *= shape[i];
+  }
+  if (t.n % per != 0)
+    fail("gguf: the tensor has " + std::to_string(t.n) + " elements, not a multiple of " +
+         std::to_string(per));
+  t.raw_bytes = t.n / per * bytes;
+  if (int64_t(raw->nbytes()) != t.raw_bytes)
+    fail("gguf: " + std::to_string(raw->nbytes()) + " raw bytes given, a tensor of shape " +
+         shape_str(t.shape) + " needs " + std::to_string(t.raw_bytes));
+  return t;
+}
+
+} // namespace
+
+extern "C" {
+
+int sdq_gguf_dequantize(sdq_array *res, sdq_array raw, int ggml_type, const int *shape, int ndim,
+                        sdq_stream s) {
+  SDQ_GUARD("gguf_dequantize", {
+    StreamImpl *st = stream_of(s, "gguf_dequantize");
+    if (!res) fail("result pointer is NULL");
+    ArrayImpl *ra = array_of(raw, "gguf_dequantize", "raw");
+    same_device(ra, st, "raw");
+    const GgufTensor t = gguf_tensor(ra, ggml_type, shape, ndim);
+    order_after(ra, st);
+    auto out = make_array(t.shape, SDQ_FLOAT32, *st);
+    kern::gguf_dequantize(static_cast<const uint8_t *>(ra->data()), ggml_type, t.n, t.raw_bytes,
+                          static_cast<float *>(out->data()), st->stream);
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_gguf_quantize(sdq_vector_array *res, sdq_array raw, int ggml_type, const int *shape,
+                      int ndim, sdq_optional_int group_size, sdq_optional_int bits,
+                      sdq_stream s) {
+  SDQ_GUARD("gguf_quantize", {
+    StreamImpl *st = stream_of(s, "gguf_quantize");
+    if (!res) fail("result pointer is NULL");
+    const int gs = opt_or(group_size, 64);
+    const int nb = opt_or(bits, 4);
+    check_group_bits(gs, nb);
+    ArrayImpl *ra = array_of(raw, "gguf_quantize", "raw");
+    same_device(ra, st, "raw");
+    const GgufTensor t = gguf_tensor(ra, ggml_type, shape, ndim);
+    if (t.shape.size() < 2)
+      fail("The matrix to be quantized must have at least 2 dimensions but it has only " +
+           std::to_string(t.shape.size()) + ".");
+    const int K = t.shape.back();
+    if (K % gs != 0)
+      fail("The last dimension of the matrix needs to be divisible by the quantization "
+           "group size " +
+           std::to_string(gs) + ". However the provided matrix has shape " + shape_str(t.shape));
+    order_after(ra, st);
+    std::vector<int> qshape = t.shape, sshape = t.shape;
+    qshape.back() = int(int64_t(K) * nb / 32);
+    sshape.back() = K / gs;
+    auto wq = make_array(qshape, SDQ_UINT32, *st);
+    auto sc = make_array(sshape, SDQ_FLOAT32, *st);
+    auto bi = make_array(sshape, SDQ_FLOAT32, *st);
+    const int64_t rows = K ? t.n / K : 0;
+    kern::gguf_quantize(static_cast<const uint8_t *>(ra->data()), ggml_type, rows, K, t.raw_bytes, gs,
+                        nb, static_cast<uint32_t *>(wq->data()), static_cast<float *>(sc->data()),
+                        static_cast<float *>(bi->data()), st->stream);
+    std::vector<std::unique_ptr<ArrayImpl>> parts;
+    parts.push_back(std::move(wq));
+    parts.push_back(std::move(sc));
+    parts.push_back(std::move(bi));
+    set_vector_result(res, std::move(parts));
+  });
+}
+
+} // extern "C"

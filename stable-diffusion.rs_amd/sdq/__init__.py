@@ -45,6 +45,7 @@ __all__ = [
     "COMBINE_PRODUCT",
     "f32_to_bf16_bits",
     "bf16_bits_to_f32",
+    "gguf_dequantize",
 ]
 
 LIB_PATH = Path(__file__).with_name("libsdq.so")
@@ -193,6 +194,8 @@ def _declare(L: ctypes.CDLL) -> None:
              ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
         ),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
+        "sdq_gguf_dequantize": (c_int, [P(A), A, c_int, P(c_int), c_int, S]),
+        "sdq_gguf_quantize": (c_int, [P(V), A, c_int, P(c_int), c_int, COptionalInt, COptionalInt, S]),
         "sdq_array_device_ptr": (c_vp, [A]),
         "sdq_version": (ctypes.c_char_p, []),
         "sdq_device_count": (c_int, []),
@@ -493,18 +496,41 @@ class QuantizedArray:
                            cls.QUANT_MODE, CArray(None), stream._raw),
             "quantize",
         )
+        return cls._from_vector(out, "quantize", group_size, bits)
+
+    @classmethod
+    def _from_vector(cls, out: CVectorArray, what: str, group_size: int, bits: int) -> "QuantizedArray":
+        """Takes the three arrays of a quantize result (mlx.rs:1884-1898)."""
+        L = lib()
         try:
             n = L.sdq_vector_array_size(out)
             if n != 3:
-                raise Error(f"sdq: quantize returned {n} arrays, expected weight, scales and biases")
+                raise Error(f"sdq: {what} returned {n} arrays, expected weight, scales and biases")
             parts = []
             for i in range(3):
                 a = CArray(None)
-                _check(L.sdq_vector_array_get(ctypes.byref(a), out, i), f"quantize output {i}")
+                _check(L.sdq_vector_array_get(ctypes.byref(a), out, i), f"{what} output {i}")
                 parts.append(Array(a))
         finally:
             L.sdq_vector_array_free(out)
         return cls(parts[0], parts[1], parts[2], group_size, bits)
+
+    @classmethod
+    def from_gguf_blocks(cls, raw, ggml_type: int, shape: Sequence[int], group_size: int, bits: int,
+                         stream: Stream) -> "QuantizedArray":
+        """A GGUF tensor's raw blocks decoded and quantized on the device in one
+        kernel: equal to quantize(gguf_dequantize(raw)) -- the loader's
+        dequantize -> from_slice_f32 -> quantize (quantized.rs:190-196)."""
+        L = lib()
+        ra = _raw_bytes(raw)
+        dims = (ctypes.c_int * max(1, len(shape)))(*[int(d) for d in shape])
+        out = CVectorArray(None)
+        _check(
+            L.sdq_gguf_quantize(ctypes.byref(out), ra._raw, int(ggml_type), dims, len(shape),
+                                _some_int(group_size), _some_int(bits), stream._raw),
+            "gguf_quantize",
+        )
+        return cls._from_vector(out, "gguf_quantize", group_size, bits)
 
     def dequantize(self, stream: Stream, dtype: int | None = None) -> Array:
         """The dense array (mlx.rs:1913-1945) -- for tests, not the hot path."""
@@ -575,6 +601,28 @@ class QuantizedArray:
 
 
 # ---- memory accounting (mlx.rs:1732-1826) ---------------------------------------
+
+
+def _raw_bytes(raw) -> Array:
+    """A GGUF tensor's bytes as a device uint8 array (an Array passes through)."""
+    if isinstance(raw, Array):
+        return raw
+    host = np.frombuffer(raw, dtype=np.uint8) if isinstance(raw, (bytes, bytearray, memoryview)) \
+        else np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
+    return Array.from_numpy(host, UINT8)
+
+
+def gguf_dequantize(raw, ggml_type: int, shape: Sequence[int], stream: Stream) -> Array:
+    """A GGUF tensor's raw blocks decoded to a float32 device array, as
+    Gguf::dequantize + Array::from_slice_f32 (mlx_gguf.rs:235-276,
+    quantized.rs:190-191)."""
+    L = lib()
+    ra = _raw_bytes(raw)
+    dims = (ctypes.c_int * max(1, len(shape)))(*[int(d) for d in shape])
+    out = CArray(None)
+    _check(L.sdq_gguf_dequantize(ctypes.byref(out), ra._raw, int(ggml_type), dims, len(shape), stream._raw),
+           "gguf_dequantize")
+    return Array(out)
 
 
 def _size_query(fn: str) -> int:

@@ -163,6 +163,46 @@ def from_dense_with(w: dict, bits_for: Callable[[str], int], s) -> QuantizedWeig
     return QuantizedWeights(quantized, dense)
 
 
+def from_gguf(path, bits: int, s) -> QuantizedWeights:
+    """Load a GGUF checkpoint, quantizing the large weights as they are read
+    (quantized.rs:181-216).  Each tensor's raw blocks go to the device; a
+    quantized one is decoded and quantized there in one kernel (the dense f32
+    form is never written), a dense one is decoded to float32.  Each result is
+    evaluated before the next tensor is read, as the reference does."""
+    return _from_gguf(path, bits, lambda name: name, s, "")
+
+
+def from_gguf_renamed(path, bits: int, rename: Callable[[str], Optional[str]], s) -> QuantizedWeights:
+    """from_gguf with names translated (quantized.rs:225-258): `rename` maps a
+    file name to the model's name, or None for a tensor the model skips."""
+    return _from_gguf(path, bits, rename, s, " this model recognises")
+
+
+def _from_gguf(path, bits: int, rename, s, what: str) -> QuantizedWeights:
+    from . import Error, eval as sdq_eval
+    from .gguf import Gguf
+
+    quantized = {}
+    dense = {}
+    with Gguf.open(path) as g:
+        for info in g.tensors:
+            name = rename(info.name)
+            if name is None:
+                continue
+            want = mixed(bits)(name)
+            if want >= 2 and quantizable(info.shape):
+                q = g.quantize(info, GROUP_SIZE, want, s)
+                sdq_eval([q.weight, q.scales, q.biases])
+                quantized[name] = q
+            else:
+                a = g.dequantize(info, s)
+                a.eval()
+                dense[name] = a
+    if not quantized and not dense:
+        raise Error(f"gguf: {path} carries no tensors{what}")
+    return QuantizedWeights(quantized, dense)
+
+
 def linear(x, name: str, bias, w: QuantizedWeights, s):
     """The dispatching linear (quantized.rs:298-318)."""
     from . import Error
