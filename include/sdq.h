@@ -312,6 +312,68 @@ int sdq_gguf_quantize(sdq_vector_array *res, sdq_array raw, int ggml_type,
                       const int *shape, int ndim, sdq_optional_int group_size,
                       sdq_optional_int bits, sdq_stream s);
 
+/* ---- the ops around the linears in a Flux block ----------------------------- */
+
+/* replaces mlx_fast_layer_norm (mlx.rs:219-227; Array::layer_norm,
+ * mlx.rs:1059-1085): y = (x - mean) / sqrt(var + eps) [* weight] [+ bias]
+ * over the last axis (at most 8192 values).  weight, bias: that many values
+ * or a NULL-ctx handle.  y has x's dtype; statistics are f32. */
+int sdq_fast_layer_norm(sdq_array *res, sdq_array x, sdq_array weight,
+                        sdq_array bias, float eps, sdq_stream s);
+
+/* replaces mlx_fast_rms_norm (mlx.rs:212-218; Array::rms_norm,
+ * mlx.rs:1095-1115): y = x / sqrt(mean(x^2) + eps) [* weight]. */
+int sdq_fast_rms_norm(sdq_array *res, sdq_array x, sdq_array weight,
+                      float eps, sdq_stream s);
+
+/* replaces mlx_fast_scaled_dot_product_attention (mlx.rs:228-238; Array::
+ * sdpa / sdpa_causal / sdpa_masked, mlx.rs:1119-1197):
+ * softmax(scale * q k^T [+ mask]) v.  queries [B, Hq, Nq, D], keys and
+ * values [B, Hk, Nk, D] with Hq a multiple of Hk and D 64 or 128.
+ * mask_mode "" or NULL: none; "causal": key j visible to query i when
+ * j <= i + Nk - Nq; "array": mask_arr, a float additive mask broadcastable
+ * to [B, Hq, Nq, Nk] over its leading axes.  sinks must be empty.  The
+ * products run as bf16 MFMAs (inputs rounded to bf16) with f32 softmax and
+ * accumulation; the result has the queries' dtype. */
+int sdq_fast_scaled_dot_product_attention(sdq_array *res, sdq_array queries,
+                                          sdq_array keys, sdq_array values,
+                                          float scale, const char *mask_mode,
+                                          sdq_array mask_arr, sdq_array sinks,
+                                          sdq_stream s);
+
+/* Flux's norm_modulate (flux.rs:255-275) as one pass:
+ * y = layer_norm(x, eps) * (1 + scale) + shift, x [B, N, C] (C <= 8192),
+ * shift and scale [B, 1, C] (a modulation triple's rows, flux.rs:279-299).
+ * The reference composes mlx_fast_layer_norm, mlx_add and mlx_multiply; y
+ * has x's dtype and is rounded once. */
+int sdq_flux_norm_modulate(sdq_array *res, sdq_array x, sdq_array shift,
+                           sdq_array scale, float eps, sdq_stream s);
+
+/* Flux's interleaved rotary embedding `rotate` (flux.rs:165-205):
+ * x [B, H, N, D], cos and sin [1, N, D/2] float32 (Rope, flux.rs:120-156);
+ * pairs (x[2i], x[2i+1]) become (e cos - o sin, e sin + o cos).  y has x's
+ * dtype. */
+int sdq_flux_rope(sdq_array *res, sdq_array x, sdq_array cos, sdq_array sin,
+                  sdq_stream s);
+
+/* A Flux block's attention from its qkv linear output(s) to merged heads, as
+ * one call: split_qkv -> qk_norm (RMS over each head, times the norm
+ * scale) -> concat -> rotate -> sdpa -> merge_heads (flux.rs:300-327,
+ * 352-381 for the double block, 446-461 for the single block).  qkv_a
+ * [B, Na, >= 3*heads*128] holds q, k, v of each token in its first
+ * 3*heads*128 columns ([3, heads, 128]); the single block passes linear1's
+ * output, whose MLP columns follow.  qkv_b (NULL ctx for none) is the second
+ * stream, appended after qkv_a along the tokens (the double block passes
+ * text as a and image as b, flux.rs:375-379), with its own norm scales.
+ * pe_cos/pe_sin: [1, Na+Nb, 64] float32.  Result [B, Na+Nb, heads*128] in
+ * qkv_a's dtype.  q, k and v are rounded to bf16 for the attention's
+ * MFMAs.  No mlx-c counterpart: the reference issues these as separate
+ * calls. */
+int sdq_flux_attention(sdq_array *res, sdq_array qkv_a, sdq_array q_norm_a,
+                       sdq_array k_norm_a, sdq_array qkv_b, sdq_array q_norm_b,
+                       sdq_array k_norm_b, sdq_array pe_cos, sdq_array pe_sin,
+                       int heads, float scale, float eps, sdq_stream s);
+
 /* ---- raw-pointer entry point ------------------------------------------------- */
 
 /* The kernel behind sdq_quantized_matmul on caller-owned device memory:

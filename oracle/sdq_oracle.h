@@ -16,6 +16,8 @@
  *   - Array::gelu_approx               crates/sd-tensor/src/mlx.rs:1041-1054
  *   - GGUF block decoders (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)
  *       crates/sd-tensor/src/mlx_gguf.rs:27-438 (sdq_oracle_gguf.c)
+ *   - layer/RMS norm, norm_modulate, RoPE, the rotary tables and attention
+ *       mlx.rs:1059-1197, sd-models/src/mlx/flux.rs:125-327 (sdq_oracle_block.c)
  *
  * Pinning status of each function is recorded beside it and in the tests
  * (tests/test_oracle.py).  Every function here is checked there against
@@ -110,6 +112,26 @@ float sdo_gguf_f16(uint16_t h);
  * out, as Gguf::dequantize does (mlx_gguf.rs:235-276).  Returns 0, or -1 on
  * an unsupported type or a size mismatch. */
 int sdo_gguf_dequantize(const uint8_t *raw, size_t raw_bytes, int type, int64_t n, float *out);
+
+/* ---- the ops around the Flux block linears (sdq_oracle_block.c) -------- */
+/* x, out: [rows, C] f32; w, b: C values or NULL.  Statistics in f64. */
+void sdo_layer_norm(const float *x, int64_t rows, int64_t C, float eps, const float *w, const float *b,
+                    float *out);
+void sdo_rms_norm(const float *x, int64_t rows, int64_t C, float eps, const float *w, float *out);
+/* x [B, N, C]; shift, scale [B, C]: layer_norm(x) * (1 + scale) + shift. */
+void sdo_norm_modulate(const float *x, int64_t B, int64_t N, int64_t C, float eps, const float *shift,
+                       const float *scale, float *out);
+/* Interleaved RoPE of x [rows, D], row r at position r % N; cs, sn [N, D/2]. */
+void sdo_rope(const float *x, int64_t rows, int64_t D, int64_t N, const float *cs, const float *sn, float *out);
+/* Rotary tables [seq, sum(axes_dim)/2] of ids [seq, n_axes] (flux.rs:126-156). */
+int sdo_embed_nd(const float *ids, int64_t seq, const int64_t *axes_dim, int64_t n_axes, float theta, float *cs,
+                 float *sn);
+/* softmax(scale q k^T + mask) v in f64; q [B,Hq,Nq,D], k, v [B,Hk,Nk,D];
+ * mode 0 none, 1 causal (key j > i + causal_offset masked), 2 additive f32
+ * mask at b*m_sb + h*m_sh + i*m_sq + j.  Returns 0, or -1 on bad sizes. */
+int sdo_sdpa(const float *q, const float *k, const float *v, int64_t B, int64_t Hq, int64_t Hk, int64_t Nq,
+             int64_t Nk, int64_t D, float scale, int mode, int64_t causal_offset, const float *mask, int64_t m_sb,
+             int64_t m_sh, int64_t m_sq, float *out);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,20 @@ def lib() -> ctypes.CDLL:
         L.sdo_resident_bytes.argtypes = [i64, i64, c_int, c_int]
         L.sdo_gelu_approx.restype = None
         L.sdo_gelu_approx.argtypes = [vp, vp, ctypes.c_size_t]
+        fp = vp
+        L.sdo_layer_norm.restype = None
+        L.sdo_layer_norm.argtypes = [fp, i64, i64, ctypes.c_float, fp, fp, fp]
+        L.sdo_rms_norm.restype = None
+        L.sdo_rms_norm.argtypes = [fp, i64, i64, ctypes.c_float, fp, fp]
+        L.sdo_norm_modulate.restype = None
+        L.sdo_norm_modulate.argtypes = [fp, i64, i64, i64, ctypes.c_float, fp, fp, fp]
+        L.sdo_rope.restype = None
+        L.sdo_rope.argtypes = [fp, i64, i64, i64, fp, fp, fp]
+        L.sdo_embed_nd.restype = c_int
+        L.sdo_embed_nd.argtypes = [fp, i64, fp, i64, ctypes.c_float, fp, fp]
+        L.sdo_sdpa.restype = c_int
+        L.sdo_sdpa.argtypes = [fp, fp, fp, i64, i64, i64, i64, i64, i64, ctypes.c_float, c_int, i64, fp,
+                               i64, i64, i64, fp]
         L.sdo_gguf_block.restype = c_int
         L.sdo_gguf_block.argtypes = [c_int, ctypes.POINTER(i64), ctypes.POINTER(i64)]
         L.sdo_gguf_f16.restype = ctypes.c_float
@@ -218,4 +232,87 @@ def gguf_dequantize(raw, ggml_type: int, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     if lib().sdo_gguf_dequantize(_p(raw), raw.size, ggml_type, n, _p(out)) != 0:
         raise ValueError("oracle gguf_dequantize rejected its arguments")
+    return out
+
+
+# ---- ops around the Flux block linears (sdq_oracle_block.c) ----------------
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _opt(a):
+    return None if a is None else _f32(a)
+
+
+def _pn(a):
+    return None if a is None else _p(a)
+
+
+def layer_norm(x, eps: float, w=None, b=None) -> np.ndarray:
+    x, w, b = _f32(x), _opt(w), _opt(b)
+    C = x.shape[-1]
+    out = np.empty_like(x)
+    lib().sdo_layer_norm(_p(x), x.size // C, C, eps, _pn(w), _pn(b), _p(out))
+    return out
+
+
+def rms_norm(x, eps: float, w=None) -> np.ndarray:
+    x, w = _f32(x), _opt(w)
+    C = x.shape[-1]
+    out = np.empty_like(x)
+    lib().sdo_rms_norm(_p(x), x.size // C, C, eps, _pn(w), _p(out))
+    return out
+
+
+def norm_modulate(x, shift, scale, eps: float) -> np.ndarray:
+    """x [B, N, C]; shift, scale [B, 1, C] (flux.rs:255-275)."""
+    x, shift, scale = _f32(x), _f32(shift), _f32(scale)
+    B, N, C = x.shape
+    out = np.empty_like(x)
+    lib().sdo_norm_modulate(_p(x), B, N, C, eps, _p(shift), _p(scale), _p(out))
+    return out
+
+
+def rope(x, cos, sin) -> np.ndarray:
+    """x [..., N, D]; cos, sin [N, D/2] (flux.rs:165-205)."""
+    x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+    N, D = x.shape[-2], x.shape[-1]
+    out = np.empty_like(x)
+    lib().sdo_rope(_p(x), x.size // D, D, N, _p(cos), _p(sin), _p(out))
+    return out
+
+
+def embed_nd(ids, axes_dim, theta: float):
+    """(cos, sin) [seq, sum(axes_dim)/2] for ids [seq, n_axes] (flux.rs:126-156)."""
+    ids = _f32(ids)
+    seq, n_axes = ids.shape
+    dims = np.ascontiguousarray(axes_dim, dtype=np.int64)
+    half = int(dims.sum()) // 2
+    cs = np.empty((seq, half), np.float32)
+    sn = np.empty((seq, half), np.float32)
+    if lib().sdo_embed_nd(_p(ids), seq, _p(dims), n_axes, theta, _p(cs), _p(sn)) != 0:
+        raise ValueError("oracle embed_nd rejected its arguments")
+    return cs, sn
+
+
+def sdpa(q, k, v, scale: float, mode: str = "", mask=None, causal_offset=None) -> np.ndarray:
+    """softmax(scale q k^T + mask) v in f64; q [B,Hq,Nq,D], k, v [B,Hk,Nk,D];
+    mask broadcastable to [B, Hq, Nq, Nk]; causal: key j is visible to query
+    i when j <= i + causal_offset (default Nk - Nq)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Hq, Nq, D = q.shape
+    Hk, Nk = k.shape[1], k.shape[2]
+    out = np.empty_like(q)
+    m = {"": 0, "causal": 1, "array": 2}[mode]
+    mp, sb, sh, sq = None, 0, 0, 0
+    if m == 2:
+        full = np.broadcast_to(_f32(mask), (B, Hq, Nq, Nk))
+        mk = _f32(full)
+        mp, sb, sh, sq = _p(mk), Hq * Nq * Nk, Nq * Nk, Nk
+    off = Nk - Nq if causal_offset is None else causal_offset
+    rc = lib().sdo_sdpa(_p(q), _p(k), _p(v), B, Hq, Hk, Nq, Nk, D, scale, m, off, mp, sb, sh, sq, _p(out))
+    if rc != 0:
+        raise ValueError("oracle sdpa rejected its arguments")
     return out

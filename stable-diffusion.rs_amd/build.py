@@ -59,11 +59,14 @@ def _combo_flags(c):
 SOURCES = [
     (CSRC / "sdq_runtime.cpp", [], None),
     (CSRC / "sdq_ops.cpp", [], None),
+    (CSRC / "sdq_ops_block.cpp", [], None),
     (CSRC / "sdq_noalloc.hip", [], None),
     (CSRC / "kernels" / "quant.hip", ["-ffp-contract=off"], None),
     (CSRC / "kernels" / "gguf.hip", ["-ffp-contract=off"], None),
     (CSRC / "kernels" / "elementwise.hip", [], None),
     (CSRC / "kernels" / "dense.hip", [], None),
+    (CSRC / "kernels" / "attention.hip", [], None),
+    (CSRC / "kernels" / "norm.hip", ["-ffp-contract=off"], None),
     (CSRC / "kernels" / "qmv.hip", [], None),
     (CSRC / "kernels" / "qmm.hip", [], None),
 ] + [

@@ -127,6 +127,70 @@ void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          int bits, const QmmPlan &plan, const SplitWorkspace &ws, const Epilogue &ep,
          hipStream_t stream);
 
+// Fused attention (attention.hip): out = softmax(scale q k^T [+ mask]) v.
+// q, k: bf16 [B, H(k: H/group), N, D] rows of D contiguous elements (row
+// strides q_sn / k_sn, head and batch strides *_sh / *_sb); vt: bf16 V^T
+// [B, H/group, D, v_sd] with keys contiguous, v_sd a multiple of 64 and the
+// padding keys zero; o: [B, H, Nq, D] by its strides, in the launch's output
+// dtype.  mode 0: no mask; 1: causal (key <= query + causal_offset); 2: an
+// additive mask of mask_dtype indexed [b * m_sb + h * m_sh + q * m_sq + key].
+struct AttnArgs {
+  const uint16_t *q = nullptr;
+  const uint16_t *k = nullptr;
+  const uint16_t *vt = nullptr;
+  void *o = nullptr;
+  int64_t q_sb = 0, q_sh = 0, q_sn = 0;
+  int64_t k_sb = 0, k_sh = 0, k_sn = 0;
+  int64_t v_sb = 0, v_sh = 0, v_sd = 0;
+  int64_t o_sb = 0, o_sh = 0, o_sn = 0;
+  int B = 0, H = 0, group = 1, Nq = 0, Nk = 0, D = 0;
+  float scale_log2 = 0.0f; // scale * log2(e)
+  int mode = 0;
+  int causal_offset = 0;
+  const void *mask = nullptr;
+  int mask_dtype = 0;
+  int64_t m_sb = 0, m_sh = 0, m_sq = 0;
+  int q_blocks = 0; // set by attention()
+};
+void attention(const AttnArgs &a, int o_dtype, hipStream_t stream);
+// The V^T row length attention() needs for nk keys.
+int64_t attention_vt_stride(int64_t nk);
+// V [bh, n, d] (float dtype, row stride ld, head stride v_sbh) -> bf16 V^T
+// [bh, d, ldt] (head stride vt_sbh), keys [n, ldt) zero-filled.
+void transpose_v(const void *v, int v_dtype, int64_t bh, int64_t n, int64_t d, int64_t v_sbh, int64_t ld,
+                 uint16_t *vt, int64_t vt_sbh, int64_t ldt, hipStream_t stream);
+
+// Row normalisations and the rotary embedding (norm.hip).  x, y: [rows, C]
+// row-major (float32/bfloat16/float16); parameters of p_dtype.
+// y = (x - mean) * rsqrt(var + eps) [* w] [+ b]   (w, b: C values or NULL)
+void layer_norm(const void *x, int x_dtype, void *y, int y_dtype, int64_t rows, int C, float eps, const void *w,
+                const void *b, int p_dtype, hipStream_t stream);
+// y = x * rsqrt(mean(x^2) + eps) [* w]
+void rms_norm(const void *x, int x_dtype, void *y, int y_dtype, int64_t rows, int C, float eps, const void *w,
+              int p_dtype, hipStream_t stream);
+// y = layer_norm(x) * (1 + scale[g]) + shift[g], g = row / rows_per_group;
+// shift, scale: [groups, C].
+void norm_modulate(const void *x, int x_dtype, void *y, int y_dtype, int64_t rows, int C, float eps,
+                   const void *shift, const void *scale, int p_dtype, int64_t rows_per_group, hipStream_t stream);
+// Interleaved rotary embedding of x [rows, D] whose row r is position
+// r % N: pairs (x[2i], x[2i+1]) rotated by (cos, sin)[n, i]; cs, sn: [N, D/2] f32.
+void rope(const void *x, int x_dtype, void *y, int64_t rows, int D, int N, const float *cs, const float *sn,
+          hipStream_t stream);
+// One source of the Flux attention input: qkv rows [B, n, >= 3*H*128]
+// (token stride ld, batch stride sb, elements) and the q/k RMSNorm scales.
+struct FluxPrepSrc {
+  const void *qkv = nullptr;
+  int64_t ld = 0, sb = 0;
+  const void *qn = nullptr;
+  const void *kn = nullptr;
+};
+// Tokens [0, na) from a, [na, na + nb) from b: q, k = rope(rms_norm(.) * scale)
+// as bf16 [B, H, na + nb, 128]; v as bf16 V^T [B, H, 128, ldt] (ldt a multiple
+// of 64, padding zero).  cs, sn: [na + nb, 64] f32.
+void flux_attention_prep(const FluxPrepSrc &a, const FluxPrepSrc &b, int x_dtype, int w_dtype, int na, int nb, int B,
+                         int H, float eps, const float *cs, const float *sn, uint16_t *q, uint16_t *k, uint16_t *vt,
+                         int64_t ldt, hipStream_t stream);
+
 // Elementwise helpers (elementwise.hip).  n = element count.
 void astype(const void *a, int a_dtype, void *out, int out_dtype, int64_t n,
             hipStream_t stream);

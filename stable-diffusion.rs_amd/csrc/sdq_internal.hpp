@@ -123,6 +123,12 @@ void set_vector_result(sdq_vector_array *res,
                        std::vector<std::unique_ptr<ArrayImpl>> values);
 std::string shape_str(const std::vector<int> &shape);
 
+// Orders stream `s` after the work producing `a` and records `s` as a user
+// of its memory (sdq_ops.cpp).
+void order_after(const ArrayImpl *a, const StreamImpl *s);
+// Fails unless `a` lives on the stream's device.
+void same_device(const ArrayImpl *a, const StreamImpl *s, const char *name);
+
 // Reports `msg` for op `op` through the installed handler.
 void report(const char *op, const char *msg);
 

@@ -12,7 +12,6 @@
 #include "sdq_internal.hpp"
 
 namespace sdq {
-namespace {
 
 // Waits on `s` for the work that produced `a`, when that ran elsewhere, and
 // records `s` as a user of a's memory, so that the allocator orders a later
@@ -32,6 +31,8 @@ void same_device(const ArrayImpl *a, const StreamImpl *s, const char *name) {
     fail(std::string("`") + name + "` lives on device " + std::to_string(a->device) +
          " but the stream is on device " + std::to_string(s->device));
 }
+
+namespace {
 
 int opt_or(sdq_optional_int v, int dflt) { return v.has_value ? v.value : dflt; }
 

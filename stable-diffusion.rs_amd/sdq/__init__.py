@@ -195,6 +195,14 @@ def _declare(L: ctypes.CDLL) -> None:
         ),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
         "sdq_gguf_dequantize": (c_int, [P(A), A, c_int, P(c_int), c_int, S]),
+        "sdq_fast_layer_norm": (c_int, [P(A), A, A, A, ctypes.c_float, S]),
+        "sdq_fast_rms_norm": (c_int, [P(A), A, A, ctypes.c_float, S]),
+        "sdq_fast_scaled_dot_product_attention": (
+            c_int, [P(A), A, A, A, ctypes.c_float, ctypes.c_char_p, A, A, S]),
+        "sdq_flux_norm_modulate": (c_int, [P(A), A, A, A, ctypes.c_float, S]),
+        "sdq_flux_rope": (c_int, [P(A), A, A, A, S]),
+        "sdq_flux_attention": (
+            c_int, [P(A), A, A, A, A, A, A, A, A, c_int, ctypes.c_float, ctypes.c_float, S]),
         "sdq_gguf_quantize": (c_int, [P(V), A, c_int, P(c_int), c_int, COptionalInt, COptionalInt, S]),
         "sdq_array_device_ptr": (c_vp, [A]),
         "sdq_version": (ctypes.c_char_p, []),
@@ -446,6 +454,38 @@ class Array:
         """self @ w.T, the dense linear of sd-models/src/mlx/mod.rs:181-189."""
         return self._binary("sdq_matmul_nt", "matmul", w, stream)
 
+    def layer_norm(self, weight: "Array | None", bias: "Array | None", eps: float, stream: Stream) -> "Array":
+        """Layer norm over the last axis (mlx.rs:1059-1085)."""
+        out = CArray(None)
+        _check(lib().sdq_fast_layer_norm(ctypes.byref(out), self._raw, _h(weight), _h(bias), eps, stream._raw),
+               "layer_norm")
+        return Array(out)
+
+    def rms_norm(self, weight: "Array | None", eps: float, stream: Stream) -> "Array":
+        """RMS norm over the last axis (mlx.rs:1095-1115)."""
+        out = CArray(None)
+        _check(lib().sdq_fast_rms_norm(ctypes.byref(out), self._raw, _h(weight), eps, stream._raw), "rms_norm")
+        return Array(out)
+
+    def _sdpa(self, keys: "Array", values: "Array", scale: float, mode: bytes, mask: "Array | None",
+              stream: Stream, what: str) -> "Array":
+        out = CArray(None)
+        _check(lib().sdq_fast_scaled_dot_product_attention(ctypes.byref(out), self._raw, keys._raw, values._raw,
+                                                           scale, mode, _h(mask), CArray(None), stream._raw), what)
+        return Array(out)
+
+    def sdpa(self, keys: "Array", values: "Array", scale: float, stream: Stream) -> "Array":
+        """Unmasked attention over [batch, heads, seq, head_dim] (mlx.rs:1161-1163)."""
+        return self._sdpa(keys, values, scale, b"", None, stream, "sdpa")
+
+    def sdpa_causal(self, keys: "Array", values: "Array", scale: float, stream: Stream) -> "Array":
+        """Causal attention, CLIP's text tower (mlx.rs:1151-1159)."""
+        return self._sdpa(keys, values, scale, b"causal", None, stream, "sdpa_causal")
+
+    def sdpa_masked(self, keys: "Array", values: "Array", scale: float, mask: "Array", stream: Stream) -> "Array":
+        """Attention with an additive mask, T5's position bias (mlx.rs:1119-1148)."""
+        return self._sdpa(keys, values, scale, b"array", mask, stream, "sdpa_masked")
+
     def gelu_approx(self, stream: Stream) -> "Array":
         return self._unary("sdq_gelu_approx", "gelu_approx", stream)
 
@@ -601,6 +641,11 @@ class QuantizedArray:
 
 
 # ---- memory accounting (mlx.rs:1732-1826) ---------------------------------------
+
+
+def _h(a: "Array | None") -> CArray:
+    """An optional array argument: the handle, or an empty one."""
+    return CArray(None) if a is None else a._raw
 
 
 def _raw_bytes(raw) -> Array:
