@@ -7,9 +7,11 @@
 // CLIP's causal text tower and T5's additive position bias.
 //
 // One pass over the keys with an online softmax (the score matrix never
-// leaves registers).  Block = 4 waves; each wave owns 64 queries as two
-// 32-query MFMA column tiles; the block walks the keys 64 at a time through a
-// double-buffered LDS stage shared by its waves.
+// leaves registers).  Block = 8 waves, 256 queries; each wave owns 32
+// queries (one MFMA column tile); the block walks the keys 64 at a time
+// through a double-buffered LDS stage shared by its waves.  A wave needs
+// under 256 registers, so two waves share each SIMD and one wave's softmax
+// (VALU, exp) runs under the other's MFMAs.
 //
 // Layout trick.  Scores are computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x16_bf16: a lane's accumulator column is ONE query and its
@@ -25,8 +27,10 @@
 //
 // Numerics: q, k, v enter the MFMAs as bf16 (rounded to nearest even by
 // the caller's conversion), P is rounded to bf16, every product and sum
-// accumulates in f32, exp is exp2 of log2(e)-scaled scores.
+// accumulates in f32, exp is exp2 of log2(e)-scaled scores.  The kernel
+// is built with contraction on (the score scaling is an explicit fma).
 #include <cmath>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -39,16 +43,36 @@ namespace {
 using namespace dev;
 using kern::AttnArgs;
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kQW = 64;            // queries per wave
-constexpr int kBQ = kWaves * kQW;  // queries per block
+// QT 32-query column tiles per wave and 8 / QT waves per block: every
+// block owns kBQ = 256 queries.  QT = 1 keeps a wave's registers under 256,
+// so two waves share each SIMD and one's softmax overlaps the other's MFMAs.
+constexpr int kBQ = 256;           // queries per block
 constexpr int kBK = 64;            // keys per iteration
+template <int QT> struct Shape {
+  static constexpr int kWaves = 8 / QT;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kQW = 32 * QT;  // queries per wave
+};
+constexpr int kQT = 1;
 
 enum { MODE_NONE = 0, MODE_CAUSAL = 1, MODE_ARRAY = 2 };
 
 __device__ __forceinline__ floatx16 mfma32(const u32x4 &a, const u32x4 &b, const floatx16 &c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 16-byte chunk c of LDS row `row` (ROW_BYTES long) as stored.  The LDS
+// serves a 16-byte read for 16 lanes per cycle across 256 bytes of banks;
+// the MFMA operand reads have lanes 0-15 on 16 consecutive rows, same chunk,
+// so the chunk is XOR-swizzled by row to put those rows on distinct banks:
+// by the row within 16 for 256-byte rows, and by the row pair within 8 for
+// 128-byte rows (two rows share one 256-byte bank line).
+template <int ROW_BYTES> __device__ __forceinline__ int swz(int row, int c) {
+  static_assert(ROW_BYTES == 128 || ROW_BYTES == 256, "row length");
+  if constexpr (ROW_BYTES == 256)
+    return c ^ (row & 15);
+  else
+    return c ^ ((row >> 1) & 7);
 }
 
 // LDS row of key `w` (0..63) of a tile: the MFMA row whose accumulator entry
@@ -58,8 +82,10 @@ __device__ __forceinline__ int k_row(int w) {
   return 32 * kt + 16 * s + (i < 4 ? 4 * h + i : 8 + 4 * h + (i - 4));
 }
 
-template <int D, int ODT, int MODE, int MDT>
-__global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
+template <int D, int ODT, int MODE, int MDT, int QT>
+__global__ __launch_bounds__(Shape<QT>::kThreads, 1) void flash_attn_kernel(AttnArgs a) {
+  constexpr int kThreads = Shape<QT>::kThreads;
+  constexpr int kQW = Shape<QT>::kQW;
   constexpr int kCK = D / 8;         // 16-byte chunks per K row
   constexpr int kKS = D / 16;        // MFMA k-steps of the score product
   constexpr int kDT = D / 32;        // 32-row tiles of head_dim in O^T
@@ -91,9 +117,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
 
   // Q^T operands: lane (r, h) of column tile qt holds query q0 + 32qt + r,
   // head-dim elements 16ks + 8h .. +7.
-  u32x4 qreg[2][kKS];
+  u32x4 qreg[QT][kKS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = q0 + 32 * qt + r;
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
@@ -104,15 +130,27 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
     }
   }
 
-  floatx16 oacc[kDT][2];
+  // Wait for the Q operands here, once: otherwise the wait for them is
+  // re-inserted inside the key loop, where it would also wait for every tile
+  // load in flight.
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) asm volatile("" : "+v"(qreg[qt][ks]));
+
+  floatx16 oacc[kDT][QT];
 #pragma unroll
   for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[dt][qt][e] = 0.0f;
-  float m[2] = {-INFINITY, -INFINITY};
-  float l[2] = {0.0f, 0.0f};
+  float m[QT], l[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.0f;
+  }
 
   // Keys this block needs: all, or (causal) up to its last query's diagonal.
   int k_end = a.Nk;
@@ -152,11 +190,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
       if (p < kKBytes / 16) {
         const int w = p / kCK, c = p % kCK;
         const int row = k_row(w);
-        *reinterpret_cast<u32x4 *>(base + row * (D * 2) + ((c ^ (row & 7)) * 16)) = stage_regs[j];
+        *reinterpret_cast<u32x4 *>(base + row * (D * 2) + (swz<D * 2>(row, c) * 16)) = stage_regs[j];
       } else {
         const int pv = p - kKBytes / 16;
         const int d = pv / (kBK / 8), c = pv % (kBK / 8);
-        *reinterpret_cast<u32x4 *>(base + kKBytes + d * (kBK * 2) + ((c ^ (d & 7)) * 16)) = stage_regs[j];
+        *reinterpret_cast<u32x4 *>(base + kKBytes + d * (kBK * 2) + (swz<kBK * 2>(d, c) * 16)) = stage_regs[j];
       }
     }
   };
@@ -175,67 +213,101 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
     if (t + 1 < n_tiles) load_tile(t + 1);
 
     // S^T = K Q^T for the 64 keys of this tile.
-    floatx16 sacc[2][2];
+    floatx16 sacc[2][QT];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[kt][qt][e] = 0.0f;
+    // Operands are read one k-step ahead of the MFMAs that use them, so an
+    // LDS read's latency hides under the previous step's MFMAs.
+    auto k_operand = [&](int ks, int kt) {
+      const int row = 32 * kt + r;
+      return *reinterpret_cast<const u32x4 *>(kl + row * (D * 2) + swz<D * 2>(row, 2 * ks + h) * 16);
+    };
+    u32x4 ka[2][2];
+    ka[0][0] = k_operand(0, 0);
+    ka[0][1] = k_operand(0, 1);
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int row = 32 * kt + r;
-        const int c = 2 * ks + h;
-        const u32x4 ka = *reinterpret_cast<const u32x4 *>(kl + row * (D * 2) + ((c ^ (row & 7)) * 16));
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) sacc[kt][qt] = mfma32(ka, qreg[qt][ks], sacc[kt][qt]);
+      if (ks + 1 < kKS) {
+        ka[(ks + 1) & 1][0] = k_operand(ks + 1, 0);
+        ka[(ks + 1) & 1][1] = k_operand(ks + 1, 1);
       }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) sacc[kt][qt] = mfma32(ka[ks & 1][kt], qreg[qt][ks], sacc[kt][qt]);
     }
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
-
-    // Online softmax, in the log2 domain: entry e of key tile kt is key
-    // k0 + 32kt + 16(e/8) + 8h + (e%8) for query q0 + 32qt + r.
-    u32x4 pb[2][2][2];  // [kt][s][qt]: P^T operands
+    // Online softmax in the log2 domain: entry e of key tile kt is key
+    // k0 + 32kt + 16(e/8) + 8h + (e%8) for query q0 + 32qt + r.  Keys are
+    // masked only in tiles that need it (past the last key, or past the
+    // causal diagonal of the wave's first query): a wave-uniform test.
+    // The running maximum is raised lazily -- only when some query's tile
+    // maximum exceeds it by more than 2^8 -- so the accumulators are
+    // rescaled in the first few tiles and rarely after; until then a
+    // probability is at most 2^8, exact enough in bf16 and f32.
+    // Entry e's key offset within the tile, less 8h, is the constant
+    // c(e) = 32kt + 16(e/8) + e%8; it is masked when c(e) >= lim.  Tiles
+    // that need no mask get a limit no entry reaches.
+    const bool need_mask = k0 + kBK > a.Nk ||
+                           (MODE == MODE_CAUSAL && k0 + kBK - 1 > q0 + a.causal_offset);
+    const int lim_keys = need_mask ? a.Nk - k0 - 8 * h : kBK;
+    u32x4 pb[2][2][QT];  // [kt][s][qt]: P^T operands
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       const int qi = q0 + 32 * qt + r;
-      float tv[2][16];
+      float sv[2][16];
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
+          float v = sacc[kt][qt][e];
           const int key = k0 + 32 * kt + 16 * (e >> 3) + 8 * h + (e & 7);
-          float v = sacc[kt][qt][e] * a.scale_log2;
           if constexpr (MODE == MODE_ARRAY) {
             const typename Elem<MDT>::T *mrow =
                 static_cast<const typename Elem<MDT>::T *>(a.mask) + int64_t(b) * a.m_sb +
                 int64_t(hh) * a.m_sh + int64_t(min(qi, a.Nq - 1)) * a.m_sq;
-            v += (key < a.Nk ? Elem<MDT>::load(mrow[key]) : 0.0f) * 1.4426950408889634f;
+            v = fmaf(v, a.scale_log2, (key < a.Nk ? Elem<MDT>::load(mrow[key]) : 0.0f) * 1.4426950408889634f);
           }
-          bool masked = key >= a.Nk;
-          if constexpr (MODE == MODE_CAUSAL) masked = masked || key > qi + a.causal_offset;
-          v = masked ? -INFINITY : v;
-          tv[kt][e] = v;
+          const int ce = 32 * kt + 16 * (e >> 3) + (e & 7);
+          if constexpr (MODE == MODE_CAUSAL) {
+            // keys past the diagonal too: key <= qi + offset
+            const int lim = min(lim_keys, need_mask ? qi + a.causal_offset + 1 - k0 - 8 * h : kBK);
+            v = ce >= lim ? -INFINITY : v;
+          } else {
+            v = ce >= lim_keys ? -INFINITY : v;
+          }
+          sv[kt][e] = v;
           mx = fmaxf(mx, v);
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m[qt], mx);
-      // A query with no unmasked key yet keeps the state at zero.
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
-      m[qt] = m_new;
+      // Raw scores are scaled by the positive scale_log2 after the maximum.
+      if constexpr (MODE != MODE_ARRAY) mx = mx * a.scale_log2;
+      if (__builtin_amdgcn_ballot_w64(mx > m[qt] + 8.0f) != 0) {
+        const float m_new = fmaxf(m[qt], mx);
+        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - m_new);
+        m[qt] = m_new;
+        l[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[dt][qt][e] *= alpha;
+      }
+      // A query with no unmasked key yet keeps its state at zero.
+      const float m_use = m[qt] == -INFINITY ? 0.0f : m[qt];
       float sum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         float p[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(tv[kt][e] - m_use);
+          const float t = MODE == MODE_ARRAY ? sv[kt][e] - m_use : fmaf(sv[kt][e], a.scale_log2, -m_use);
+          p[e] = __builtin_amdgcn_exp2f(t);
           sum += p[e];
         }
 #pragma unroll
@@ -243,28 +315,28 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) pb[kt][s][qt][w] = pack_bf16x2(p[8 * s + 2 * w], p[8 * s + 2 * w + 1]);
       }
-      l[qt] = l[qt] * alpha + sum;
-#pragma unroll
-      for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[dt][qt][e] *= alpha;
+      l[qt] += sum;
     }
 
-    // O^T += V^T P^T.
-#pragma unroll
-    for (int dt = 0; dt < kDT; ++dt) {
+    // O^T += V^T P^T, operands again read one step ahead.
+    auto v_operand = [&](int i) {  // i = (dt, kt, s) flattened
+      const int dt = i >> 2, kt = (i >> 1) & 1, s = i & 1;
       const int row = 32 * dt + r;
+      return *reinterpret_cast<const u32x4 *>(vl + row * (kBK * 2) + swz<kBK * 2>(row, 4 * kt + 2 * s + h) * 16);
+    };
+    constexpr int kVSteps = kDT * 4;
+    u32x4 va[2];
+    va[0] = v_operand(0);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int i = 0; i < kVSteps; ++i) {
+      if (i + 1 < kVSteps) va[(i + 1) & 1] = v_operand(i + 1);
+      const int dt = i >> 2, kt = (i >> 1) & 1, s = i & 1;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int c = 4 * kt + 2 * s + h;
-          const u32x4 va = *reinterpret_cast<const u32x4 *>(vl + row * (kBK * 2) + ((c ^ (row & 7)) * 16));
-#pragma unroll
-          for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = mfma32(va, pb[kt][s][qt], oacc[dt][qt]);
-        }
-      }
+      for (int qt = 0; qt < QT; ++qt) oacc[dt][qt] = mfma32(va[i & 1], pb[kt][s][qt], oacc[dt][qt]);
     }
+    // The next tile's K and V^T go to the other stage last, leaving the
+    // whole iteration for their global loads.
+    if (t + 1 < n_tiles) store_tile(buf ^ 1);
     __syncthreads();
   }
 
@@ -272,7 +344,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_attn_kernel(AttnArgs a) {
   using OT = typename Elem<ODT>::T;
   OT *op = static_cast<OT *>(a.o) + int64_t(b) * a.o_sb + int64_t(hh) * a.o_sh;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = q0 + 32 * qt + r;
     const float lt = l[qt] + __shfl_xor(l[qt], 32);
     const float inv = 1.0f / lt;
@@ -328,7 +400,8 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const typename Elem<ID
 template <int D, int ODT, int MODE, int MDT> void launch_d(const AttnArgs &a, hipStream_t st) {
   constexpr int kStage = kBK * D * 2 * 2;
   const int blocks = a.q_blocks * a.B * a.H;
-  hipLaunchKernelGGL((flash_attn_kernel<D, ODT, MODE, MDT>), dim3(blocks), dim3(kThreads), 2 * kStage, st, a);
+  hipLaunchKernelGGL((flash_attn_kernel<D, ODT, MODE, MDT, kQT>), dim3(blocks), dim3(Shape<kQT>::kThreads),
+                     2 * kStage, st, a);
 }
 
 template <int D, int ODT, int MODE> void launch_mdt(const AttnArgs &a, hipStream_t st) {
