@@ -196,6 +196,13 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(typename Elem<D>::T *
     fail("unsupported dtype");                                               \
   }
 
+// Zeroes a run of 32-bit words (a kernel rather than hipMemsetAsync, so it
+// is also safe inside a captured graph).
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t *__restrict__ p, int64_t words) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
 } // namespace
 
 namespace kern {
@@ -286,6 +293,14 @@ void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue 
     });
   });
   hip_check(hipGetLastError(), "combine launch");
+}
+
+void fill_zero(void *p, size_t bytes, hipStream_t stream) {
+  const int64_t words = int64_t(bytes / 4);
+  if (words == 0) return;
+  const int grid = int((words + 255) / 256);
+  fill_zero_kernel<<<grid, 256, 0, stream>>>(static_cast<uint32_t *>(p), words);
+  hip_check(hipGetLastError(), "fill_zero launch");
 }
 
 } // namespace kern

@@ -78,9 +78,11 @@ inline bool epilogue_ok(const Epilogue &ep) {
 }
 
 // Workspace the large-M kernel uses when it splits K across blocks: f32
-// partial tiles, added by a second kernel.
+// partial tiles (added by a second kernel, or by the stream-K owner blocks)
+// and, for stream-K, one flag per worker, zero between launches.
 struct SplitWorkspace {
   float *partial = nullptr;
+  int *flags = nullptr;
 };
 
 // Launch plan of the small-M kernel: each block owns `tiles_per_block`
@@ -111,6 +113,7 @@ struct QmmPlan {
   int dp_tiles = 0;         // tiles [0, dp_tiles) are computed whole
   int splits = 1;           // K ranges of each later tile
   int steps_per_split = 0;  // 64-wide K steps per range
+  int sk_workers = 0;       // > 0: stream-K over this many blocks (one per CU)
   int blocks = 0;           // grid size
   size_t partial_floats = 0; // workspace needed (0 without split tiles)
 };
@@ -120,7 +123,9 @@ struct QmmPlan {
 // no-allocation entry point's fixed scratch); a split that would need more
 // is not taken.
 QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus,
-                 size_t max_partial_floats = ~size_t(0));
+                 size_t max_partial_floats = ~size_t(0), bool allow_stream_k = true);
+// Zeroes `bytes` (a multiple of 4) at `p` with a kernel on `stream`.
+void fill_zero(void *p, size_t bytes, hipStream_t stream);
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,

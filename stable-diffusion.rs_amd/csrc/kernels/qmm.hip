@@ -3,6 +3,7 @@
 // combination): the MFMA-bound side of mlx_quantized_matmul
 // (crates/sd-tensor/src/mlx.rs:386-397, 1947-1975).
 #include <algorithm>
+#include <cstdint>
 #include <string>
 
 #include "device_common.hpp"
@@ -38,7 +39,8 @@ namespace {
 
 namespace kern {
 
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_floats) {
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_floats,
+                 bool allow_stream_k) {
   QmmPlan p;
   p.bm = M <= 128 ? 128 : 256;
   p.tiles_n = int((N + qmm_detail::kTileN - 1) / qmm_detail::kTileN);
@@ -47,24 +49,27 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_fl
   const int64_t steps = K / 64;
   const int64_t slots = cus > 0 ? cus : 256; // one block per CU at a time
   const int64_t rem = p.tiles % slots;
-  // The last, partly filled round of whole tiles costs as much as a full
-  // one.  Its tiles can instead be split along K into ranges that run side
-  // by side.  Costs in thousandths of a 64-wide step of one block: a range
-  // costs its length, plus a fixed part (writing its partial tile, and the
-  // reduction kernel's launch), plus its share of the reduction kernel,
-  // which reads every partial tile once at roughly HBM speed.
+  const size_t tile_floats = size_t(p.bm) * qmm_detail::kTileN;
+  // Costs in thousandths of one block's 64-wide K step.
+  // Data-parallel: whole tiles in rounds of `slots`.  The last, partly filled
+  // round costs as much as a full one; its tiles can instead be split along
+  // K into ranges that run side by side: a range costs its length, plus a
+  // fixed part (writing its partial tile, and the reduction kernel's
+  // launch), plus its share of the reduction kernel, which reads every
+  // partial tile once at roughly HBM speed.
   constexpr int64_t kSplitFixed = 4000;
   constexpr int64_t kReducePerRange = 45;
   p.dp_tiles = p.tiles;
   p.splits = 1;
   p.steps_per_split = int(steps);
+  int64_t dp_cost = (p.tiles + slots - 1) / slots * steps * 1000;
   if (rem > 0) {
     int64_t best = steps * 1000;
     for (int64_t s = 2; s <= 16 && rem * s <= slots; ++s) {
       const int64_t sps = (steps + s - 1) / s;
       if (sps < 2) break;
       const int64_t ranges = (steps + sps - 1) / sps;
-      if (size_t(rem * ranges) * size_t(p.bm) * qmm_detail::kTileN > max_partial_floats) continue;
+      if (size_t(rem * ranges) * tile_floats > max_partial_floats) continue;
       const int64_t cost = sps * 1000 + kSplitFixed + rem * ranges * kReducePerRange;
       if (cost < best) {
         best = cost;
@@ -72,11 +77,41 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_fl
         p.steps_per_split = int(sps);
       }
     }
-    if (p.splits > 1) p.dp_tiles = int(p.tiles - rem);
+    if (p.splits > 1) {
+      p.dp_tiles = int(p.tiles - rem);
+      dp_cost = p.dp_tiles / slots * steps * 1000 + best;
+    }
+  }
+  // Stream-K: one block per CU, each taking an equal share of the
+  // tiles x steps iterations.  A tile cut between blocks costs the
+  // contributor a coherent partial-tile write and its owner one coherent
+  // read per contributor, plus a second pipeline fill; measured on MI355X
+  // at about 9 steps of a 256-row tile per partial moved (fc1 at M = 1024:
+  // 36 steps of work ran 54 step-times), so stream-K pays only for long K
+  // (Flux's fc2 and linear2 at 4096+ tokens: 5-10 % over whole tiles).
+  constexpr int64_t kSkPerPartial = 9000;
+  const int64_t T = int64_t(p.tiles) * steps;
+  const int64_t G = std::min<int64_t>(slots, T / 4);
+  if (allow_stream_k && p.bm == 256 && G >= 2 && rem > 0) {
+    const int64_t share = (T + G - 1) / G;
+    const int64_t contributors = (steps + share - 1) / share; // per cut tile, at most
+    // Every piece after a block's first refills the pipeline (~2 steps).
+    const int64_t pieces = share / steps + 2;
+    const int64_t sk_cost = share * 1000 + (1 + contributors) * kSkPerPartial + (pieces - 1) * 2000;
+    const size_t need = size_t(G) * tile_floats;
+    if (sk_cost < dp_cost && need <= max_partial_floats) {
+      p.dp_tiles = p.tiles;
+      p.splits = 1;
+      p.steps_per_split = int(steps);
+      p.sk_workers = int(G);
+      p.blocks = int(G);
+      p.partial_floats = need;
+      return p;
+    }
   }
   const int64_t sk_tiles = p.tiles - p.dp_tiles;
   p.blocks = int(p.dp_tiles + sk_tiles * p.splits);
-  p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * size_t(p.bm) * qmm_detail::kTileN;
+  p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * tile_floats;
   return p;
 }
 
@@ -101,15 +136,22 @@ void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
   // The launch must be exactly the plan for this shape: the grid, the
   // per-range K bounds and the workspace all follow from it.
   const QmmPlan want = plan_qmm(M, N, K, 0);
-  if (plan.bm != want.bm || plan.tiles_n != want.tiles_n || plan.tiles != want.tiles ||
-      plan.splits < 1 || plan.steps_per_split < 1 || plan.dp_tiles < 0 || plan.dp_tiles > plan.tiles ||
-      plan.blocks != plan.dp_tiles + (plan.tiles - plan.dp_tiles) * plan.splits ||
-      (plan.dp_tiles < plan.tiles &&
-       (int64_t(plan.splits - 1) * plan.steps_per_split >= K / 64 ||
-        int64_t(plan.splits) * plan.steps_per_split < K / 64)))
+  if (plan.bm != want.bm || plan.tiles_n != want.tiles_n || plan.tiles != want.tiles)
     fail("qmm: inconsistent launch plan");
-  if (plan.dp_tiles < plan.tiles && !ws.partial)
-    fail("qmm: split-K launch without a workspace");
+  if (plan.sk_workers > 0) {
+    if (plan.blocks != plan.sk_workers || int64_t(plan.sk_workers) > int64_t(plan.tiles) * (K / 64) ||
+        plan.dp_tiles != plan.tiles)
+      fail("qmm: inconsistent stream-K plan");
+    if (!ws.partial || !ws.flags) fail("qmm: stream-K launch without a workspace");
+  } else {
+    if (plan.splits < 1 || plan.steps_per_split < 1 || plan.dp_tiles < 0 || plan.dp_tiles > plan.tiles ||
+        plan.blocks != plan.dp_tiles + (plan.tiles - plan.dp_tiles) * plan.splits ||
+        (plan.dp_tiles < plan.tiles &&
+         (int64_t(plan.splits - 1) * plan.steps_per_split >= K / 64 ||
+          int64_t(plan.splits) * plan.steps_per_split < K / 64)))
+      fail("qmm: inconsistent launch plan");
+    if (plan.dp_tiles < plan.tiles && !ws.partial) fail("qmm: split-K launch without a workspace");
+  }
   if (!kern::epilogue_ok(ep)) fail("qmm: bad epilogue (bias dtype or activation)");
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_FLOAT32, SDQ_FLOAT32)
   SDQ_QMM_CASE(SDQ_BFLOAT16, SDQ_BFLOAT16, SDQ_BFLOAT16)

@@ -66,20 +66,26 @@ __device__ __forceinline__ u32x4 dequant8<8>(const u32x4 (&wr)[2], int i, float 
   return r;
 }
 
-// Work assignment of one launch.  Tiles are numbered M-tile major; tiles
-// [0, dp_tiles) are computed whole, one block each; each tile after that is
-// split into `splits` K ranges of `steps_per_split` 64-wide steps, one block
-// per range, each writing its f32 partial tile to `partial`
-// ([split tile][range][BM][256], row-major); qmm_reduce_kernel adds them.
+// Work assignment of one launch.  Tiles are numbered M-tile major.
+// Data-parallel (sk_workers == 0): tiles [0, dp_tiles) are computed whole,
+// one block each; each tile after that is split into `splits` K ranges of
+// `steps_per_split` 64-wide steps, one block per range, each writing its f32
+// partial tile to `partial` ([split tile][range][BM][256]);
+// qmm_reduce_kernel adds them.  Stream-K (sk_workers = G > 0): G blocks share
+// the tiles * K/64 iterations evenly (see the kernel); `partial` has G slots
+// and `flags` G ints, zero between launches.
 struct QmmWork {
   int tiles_n;
+  int tiles;
   int dp_tiles;
   int splits;
   int steps_per_split;
+  int sk_workers;
   float *partial;
+  int *flags;
 };
 
-template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH>
+template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH, bool SKM>
 __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
@@ -103,17 +109,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   const int h = lane >> 5;
   const int steps = K / 64;
   const int groups = K / GS;
-  const int bid = blockIdx.x;
-  int tile = bid, split = 0, k_begin = 0, k_end = steps;
-  if (bid >= wk.dp_tiles) {
-    const int j = bid - wk.dp_tiles;
-    tile = wk.dp_tiles + j / wk.splits;
-    split = j % wk.splits;
-    k_begin = split * wk.steps_per_split;
-    k_end = min(steps, k_begin + wk.steps_per_split);
-  }
-  const int m0 = (tile / wk.tiles_n) * BM;
-  const int nw = (tile % wk.tiles_n) * kTileN + wave * 64;
+  int m0 = 0, nw = 0;
+  floatx16 acc[MB][2];
+  // The product of tile `tile` over the K steps [k_begin, k_end), into acc.
+  auto run = [&](const int tile, const int k_begin, const int k_end) __attribute__((always_inline)) {
+  m0 = (tile / wk.tiles_n) * BM;
+  nw = (tile % wk.tiles_n) * kTileN + wave * 64;
   const int k_last = k_end - 1;
 
   // Buffer windows (byte offsets fit in 32 bits: checked on the host).
@@ -205,7 +206,6 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     }
   };
 
-  floatx16 acc[MB][2];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -363,6 +363,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     st0 = st1;
     __syncthreads();
   }
+  };
 
   // Output.  Accumulator entry e of lane (r, h) in tile (mb, j) is row
   // 32*mb + 8*(e/4) + 4*h + e%4, column 32*j + r of the wave's slab: one
@@ -434,45 +435,194 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     }
   };
 
-  if (bid >= wk.dp_tiles) {
-    // A K range of a split tile: its f32 accumulators go to the workspace in
-    // 16-byte pieces, register-major: entries 4q..4q+3 of MFMA tile (mb, j)
-    // of thread t at float4 ((mb*2 + j)*4 + q)*256 + t of the range's slot,
-    // so each store instruction writes 1 KB contiguous per wave.  Rows past M
-    // are written too and never read.  The reduction kernel that follows on
-    // the stream adds the ranges in order.
-    const int64_t slot = int64_t(tile - wk.dp_tiles) * wk.splits + split;
-    float4 *mine = reinterpret_cast<float4 *>(wk.partial + slot * (BM * kTileN)) + tid;
+  // A K range's f32 accumulators in a workspace slot of BM x 256 floats:
+  // 16-byte pieces, register-major -- entries 4q..4q+3 of MFMA tile (mb, j)
+  // of thread t at float4 ((mb*2 + j)*4 + q)*256 + t -- so each store
+  // instruction writes 1 KB contiguous per wave.  Rows past M are written too
+  // and never used.
+  // Partial tiles of the data-parallel split go through ordinary stores (the
+  // reduction kernel reads them after this kernel ends).  Stream-K partials
+  // are read by another block of this kernel, possibly on another XCD, whose
+  // L2 is not this one's: they are written and read with device-coherent
+  // (sc1) accesses, which go to the memory side instead of an XCD's L2, so
+  // no L2 write-back or invalidation is needed around the flag (both would
+  // cost every block on the XCD its cached tiles).
+  const Rsrc rp = make_rsrc(wk.partial, 0x7ffffff0u);
+  constexpr int kCoherent = 16; // the sc1 cache-policy bit
+  auto part_off = [&](int64_t slot, int reg4) {
+    return uint32_t(slot * (BM * kTileN * 4) + (int64_t(reg4) * kThreads + tid) * 16);
+  };
+  auto write_partial = [&](int64_t slot, bool coherent) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          mine[((mb * 2 + j) * 4 + q) * kThreads] =
-              float4{acc[mb][j][4 * q], acc[mb][j][4 * q + 1], acc[mb][j][4 * q + 2], acc[mb][j][4 * q + 3]};
-    return;
-  }
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 v = {__float_as_uint(acc[mb][j][4 * q]), __float_as_uint(acc[mb][j][4 * q + 1]),
+                           __float_as_uint(acc[mb][j][4 * q + 2]), __float_as_uint(acc[mb][j][4 * q + 3])};
+          const uint32_t off = part_off(slot, (mb * 2 + j) * 4 + q);
+          if (coherent)
+            __builtin_amdgcn_raw_buffer_store_b128(v, rp, off, 0, kCoherent);
+          else
+            __builtin_amdgcn_raw_buffer_store_b128(v, rp, off, 0, 0);
+        }
+  };
+  // Loads go out in batches of 16 (64 registers, free once the K loop is
+  // done): one at a time, each would wait a full trip to the memory side.
+  auto add_partial = [&](int64_t slot) {
+    constexpr int kPieces4 = MB * 2 * 4, kBatch = 16;
+#pragma unroll
+    for (int b0 = 0; b0 < kPieces4; b0 += kBatch) {
+      u32x4 v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, part_off(slot, b0 + u), 0, kCoherent));
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int reg4 = b0 + u, mb = reg4 >> 3, j = (reg4 >> 2) & 1, q = reg4 & 3;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[mb][j][4 * q + c] += __uint_as_float(v[u][c]);
+      }
+    }
+  };
 
   // The epilogue needs only the column's bias: one value per lane per 32-row
   // block of weights.  The activation is chosen once for the whole tile: a
   // per-element branch would end each element's LDS write in a wait.
-  float bcol[2];
+  auto finish_tile = [&]() __attribute__((always_inline)) {
+    float bcol[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
-  auto finish = [&](auto act) {
-    store_tile([&](int mb, int j, float (&v)[16]) {
+    for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
+    auto finish = [&](auto act) {
+      store_tile([&](int mb, int j, float (&v)[16]) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float t = acc[mb][j][e] + bcol[j];
-        v[e] = decltype(act)::value ? gelu_approx_f(t) : t;
-      }
-    });
+        for (int e = 0; e < 16; ++e) {
+          const float t = acc[mb][j][e] + bcol[j];
+          v[e] = decltype(act)::value ? gelu_approx_f(t) : t;
+        }
+      });
+    };
+    if (ep.act == 1)
+      finish(std::integral_constant<bool, true>{});
+    else
+      finish(std::integral_constant<bool, false>{});
   };
-  if (ep.act == 1)
-    finish(std::integral_constant<bool, true>{});
-  else
-    finish(std::integral_constant<bool, false>{});
+
+  // Data-parallel launch (sk_workers == 0): block b computes tile b whole,
+  // or (b past dp_tiles) one K range of a split tile, whose partial the
+  // reduction kernel that follows on the stream adds.
+  //
+  // Stream-K launch: worker g (this block) owns the iterations [lo(g),
+  // lo(g+1)) of the tile-major sequence of (tile, K step), lo(g) = g*T/G.
+  // Its range is at most three kinds of piece, done in this order:
+  //   1. the tail: a tile's K prefix that goes on in worker g+1's range --
+  //      a partial, stored in slot g, then flag g is raised;
+  //   2. the whole tiles in between, stored directly;
+  //   3. the head: the end of a tile begun by lower workers -- it waits for
+  //      their flags (raised by pieces they did first), adds their partials
+  //      in worker order (so the sum does not depend on timing) and stores
+  //      the tile.
+  // Waits point only to lower block indices, which the hardware dispatches
+  // first, so no wait depends on a block not yet running; each wait is
+  // bounded all the same (a flag that never comes leaves the tile without
+  // that partial rather than hanging).  The three kinds are three inlined
+  // copies of the K loop: a loop over mixed pieces keeps too much alive.
+  const int g = blockIdx.x;
+  if constexpr (!SKM) {
+    // Data-parallel launch: block b computes tile b whole, or (b past
+    // dp_tiles) one K range of a split tile, whose partial the reduction
+    // kernel that follows on the stream adds.  (An instantiation of its own:
+    // the stream-K piece structure costs this loop ~9 % in register
+    // allocation.)
+    int tile = g, kb = 0, ke = steps;
+    int64_t slot = -1;
+    if (g >= wk.dp_tiles) {
+      const int jb = g - wk.dp_tiles;
+      tile = wk.dp_tiles + jb / wk.splits;
+      const int split = jb % wk.splits;
+      kb = split * wk.steps_per_split;
+      ke = min(steps, kb + wk.steps_per_split);
+      slot = int64_t(tile - wk.dp_tiles) * wk.splits + split;
+    }
+    run(tile, kb, ke);
+    if (slot >= 0) {
+      write_partial(slot, false);
+      return;
+    }
+    finish_tile();
+    return;
+  }
+  const bool sk = true;
+  int tail_tile = -1, tail_kb = 0, tail_ke = 0; // a partial piece, stored in slot g
+  int64_t tail_slot = 0;
+  int full_begin = 0, full_end = 0;             // whole tiles [full_begin, full_end)
+  int head_tile = -1, head_kb = 0;              // the end of a tile begun by lower workers
+  const int G = wk.sk_workers;
+  const int64_t T = int64_t(wk.tiles) * steps;
+  auto lo_of = [&](int gg) { return int64_t(gg) * T / G; };
+  {
+    const int64_t lo = lo_of(g);
+    const int64_t hi = lo_of(g + 1);
+    // Tiles touched: [t_first, t_last]; the head is t_first when lo is
+    // inside it, the tail t_last when hi is inside it (possibly one tile).
+    const int t_first = int(lo / steps), t_last = int((hi - 1) / steps);
+    const int kb_first = int(lo - int64_t(t_first) * steps);
+    const int ke_last = int(hi - int64_t(t_last) * steps);
+    if (ke_last < steps) {
+      tail_tile = t_last;
+      tail_kb = t_first == t_last ? kb_first : 0;
+      tail_ke = ke_last;
+      tail_slot = g;
+    }
+    if (kb_first > 0 && !(tail_tile >= 0 && t_first == t_last)) {
+      head_tile = t_first;
+      head_kb = kb_first;
+    }
+    full_begin = t_first + (kb_first > 0 ? 1 : 0);
+    full_end = t_last + (ke_last < steps ? 0 : 1);
+  }
+  bool ran = false;
+  if (tail_tile >= 0) {
+    run(tail_tile, tail_kb, tail_ke);
+    write_partial(tail_slot, sk);
+    if (sk) {
+      // Every thread's coherent stores complete (s_waitcnt 0: all counters
+      // drained) before the block's flag goes up.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) __hip_atomic_store(wk.flags + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ran = true;
+  }
+  for (int tile = full_end - 1; tile >= full_begin; --tile) {
+    if (ran) __syncthreads(); // the previous piece's output staging used the LDS
+    run(tile, 0, steps);
+    finish_tile();
+    ran = true;
+  }
+  if (head_tile >= 0) {
+    if (ran) __syncthreads();
+    run(head_tile, head_kb, steps);
+    const int64_t tile_lo = int64_t(head_tile) * steps;
+    int from = g - 1;
+    while (from > 0 && lo_of(from) > tile_lo) --from;
+    for (int gg = from; gg < g; ++gg) {
+      if (tid == 0) {
+        int spins = 0;
+        // Coherent (sc1) polls: the flag is read at the memory side.
+        while (__hip_atomic_load(wk.flags + gg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+               ++spins < (1 << 22))
+          __builtin_amdgcn_s_sleep(2);
+        __hip_atomic_store(wk.flags + gg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // The partial's loads are issued only after the flag was seen (the
+      // barrier follows the poll), and read it coherently as well.
+      __syncthreads();
+      add_partial(gg);
+    }
+    finish_tile();
+  }
 }
 
 // Sum of the K ranges of the split tiles, in range order (so the result does
@@ -528,7 +678,8 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
                   const kern::Epilogue &ep, hipStream_t st) {
-  const QmmWork wk{plan.tiles_n, plan.dp_tiles, plan.splits, plan.steps_per_split, ws.partial};
+  const QmmWork wk{plan.tiles_n, plan.tiles, plan.dp_tiles, plan.splits, plan.steps_per_split, plan.sk_workers,
+                   ws.partial, ws.flags};
   const dim3 grid(plan.blocks);
   auto *yp = static_cast<typename Elem<ODT>::T *>(y);
   auto *xp = static_cast<const typename Elem<XDT>::T *>(x);
@@ -538,8 +689,19 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
   const size_t srow_bytes = size_t(K / gs) * sizeof(typename Elem<SDT>::T);
   const bool sch = srow_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(s) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(b) % 16 == 0;
-#define SDQ_QMM_LAUNCH(G, C) \
-  qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C><<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk, ep)
+#define SDQ_QMM_LAUNCH(G, C)                                                                               \
+  do {                                                                                                     \
+    if (plan.sk_workers > 0) {                                                                             \
+      if constexpr (BM == 256)                                                                             \
+        qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C, true>                                                    \
+            <<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk, ep);                          \
+      else                                                                                                 \
+        fail("qmm: stream-K plans use 256-row tiles");                                                     \
+    } else {                                                                                               \
+      qmm_kernel<BITS, XDT, SDT, ODT, BM, G, C, false>                                                     \
+          <<<grid, kThreads, 0, st>>>(yp, xp, ldx, w, sp, bp, M, N, K, wk, ep);                            \
+    }                                                                                                      \
+  } while (0)
   if (gs == 64) {
     if (sch) SDQ_QMM_LAUNCH(64, true);
     else SDQ_QMM_LAUNCH(64, false);
@@ -548,7 +710,7 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
     else SDQ_QMM_LAUNCH(128, false);
   }
 #undef SDQ_QMM_LAUNCH
-  const int sk_tiles = plan.tiles - plan.dp_tiles;
+  const int sk_tiles = plan.sk_workers ? 0 : plan.tiles - plan.dp_tiles;
   if (sk_tiles > 0) {
     hip_check(hipGetLastError(), "qmm launch");
     const int64_t threads = int64_t(sk_tiles) * BM * (kTileN / 4);

@@ -74,6 +74,10 @@ void clear_cache();
 // the stream is freed (release_stream_workspace) or the cache is cleared.
 // The per-thread handle hipStreamPerThread names a different stream in each
 // host thread, so its workspace is kept per thread.
+// The buffer starts with a header of kWorkspaceHeaderFloats floats -- the
+// stream-K flags, zeroed when the buffer is allocated and left zero by every
+// launch -- followed by partial_floats floats of partial tiles.
+constexpr size_t kWorkspaceHeaderFloats = 1024;
 float *stream_workspace(int device, hipStream_t stream, size_t partial_floats);
 void release_stream_workspace(int device, hipStream_t stream);
 

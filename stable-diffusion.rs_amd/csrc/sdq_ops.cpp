@@ -70,8 +70,11 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
   } else {
     kern::QmmPlan plan = kern::plan_qmm(M, N, K, cu_count(device));
     kern::SplitWorkspace ws;
-    if (plan.dp_tiles < plan.tiles)
-      ws.partial = stream_workspace(device, stream, plan.partial_floats);
+    if (plan.dp_tiles < plan.tiles || plan.sk_workers > 0) {
+      float *base = stream_workspace(device, stream, plan.partial_floats);
+      ws.flags = reinterpret_cast<int *>(base);
+      ws.partial = base + kWorkspaceHeaderFloats;
+    }
     // The tile kernel fuses bias and activation; the combine stage follows
     // as one in-place pass (the tile store with it grows the kernel ~6x).
     kern::Epilogue ep_mm = ep;

@@ -13,6 +13,7 @@
 #include <sstream>
 #include <thread>
 
+#include "kernels/launch.hpp"
 #include "sdq_internal.hpp"
 
 namespace sdq {
@@ -338,12 +339,15 @@ WorkspaceKey ws_key(int device, hipStream_t stream) {
 float *stream_workspace(int device, hipStream_t stream, size_t partial_floats) {
   std::lock_guard<std::mutex> lock(g_ws_mu);
   WorkspaceSlot &slot = g_ws[ws_key(device, stream)];
-  if (slot.partial_floats < partial_floats) {
+  const size_t want = partial_floats + kWorkspaceHeaderFloats;
+  if (slot.partial_floats < want) {
     // Grows by at least half again, so a growing sequence reallocates rarely;
     // the old buffer returns to the cache once the stream's work on it is done.
-    const size_t n = std::max(partial_floats, slot.partial_floats + slot.partial_floats / 2);
+    const size_t n = std::max(want, slot.partial_floats + slot.partial_floats / 2);
     slot.partial = allocate(n * sizeof(float), device, stream);
     slot.partial_floats = n;
+    // The header holds the stream-K flags, which each launch leaves zero.
+    kern::fill_zero(slot.partial->ptr, kWorkspaceHeaderFloats * sizeof(float), stream);
   }
   return slot.partial ? static_cast<float *>(slot.partial->ptr) : nullptr;
 }
