@@ -142,6 +142,9 @@ def parse():
                     help="report the unfused form (fc1, GELU kernel, fc2) as the headline")
     ap.add_argument("--only", choices=["step", "sweep", "config5"], default=None,
                     help="run one part only (for profiling its kernels)")
+    ap.add_argument("--sweep-m", default="1,4,16,32,64,128,256,512,1024,1536,4608",
+                    help="comma-separated M values of the 3072->12288 sweep")
+    ap.add_argument("--sweep-bits", default="4,8", help="comma-separated bit widths of the sweep")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, run one f32->bf16 copy of 2^27 elements (512 MiB read, "
                          "256 MiB written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -444,9 +447,9 @@ def main():
     if args.only in (None, "sweep") and not args.no_sweep:
         xs = torch.randn(4608, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
         ys = torch.empty(4608, MLP, device=dev, dtype=torch.bfloat16)
-        for bits in (4, 8):
+        for bits in (int(b) for b in args.sweep_bits.split(",")):
             layer = SynthLayer(torch, dev, MLP, HIDDEN, bits, seed=20 + bits)
-            for M in (1, 4, 16, 32, 64, 128, 256, 512, 1024, 1536, 4608):
+            for M in (int(m) for m in args.sweep_m.split(",")):
                 ms = graph_time(torch, raw, layer, M, xs, ys)
                 pt = {"M": M, "bits": bits, **roofline_point(M, MLP, HIDDEN, bits, ms), "copies": layer.rotate}
                 sweep.append(pt)

@@ -93,20 +93,33 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def _compile(src: Path, extra: list[str], name: str | None, verbose: bool) -> Path:
-    obj = BUILD / ((name or src.stem + src.suffix.replace(".", "_")) + ".o")
+    obj = _obj(src, name)
     cmd = [HIPCC, *COMMON, *extra, "-c", str(src), "-o", str(obj)]
     _run(cmd, verbose)
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
+def _obj(src: Path, name: str | None) -> Path:
+    return BUILD / ((name or src.stem + src.suffix.replace(".", "_")) + ".o")
+
+
+def build(verbose: bool = False, jobs: int | None = None, only: list[str] | None = None) -> Path:
+    """Compile every source (or, with `only`, the sources whose file names
+    start with one of the given prefixes, reusing the other objects from an
+    earlier full build) and link the library."""
     BUILD.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
     # Longest compiles first, so the pool's tail is short.
     order = sorted(SOURCES, key=lambda s: 0 if s[0].name.startswith(("qmm", "qmv")) else 1)
+    todo = [s for s in order if only is None or s[0].name.startswith(tuple(only))]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, src, extra, name, verbose) for src, extra, name in order]
-        objs = [f.result() for f in futs]
+        futs = [ex.submit(_compile, src, extra, name, verbose) for src, extra, name in todo]
+        for f in futs:
+            f.result()
+    objs = [_obj(src, name) for src, _, name in order]
+    missing = [o.name for o in objs if not o.exists()]
+    if missing:
+        raise RuntimeError(f"objects missing (run a full build first): {', '.join(missing)}")
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
@@ -116,8 +129,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--only", nargs="+", metavar="PREFIX",
+                    help="recompile only sources whose file name starts with PREFIX (others from the last build)")
     args = ap.parse_args()
-    lib = build(verbose=args.verbose)
+    lib = build(verbose=args.verbose, only=args.only)
     print(lib)
     return 0
 

@@ -135,7 +135,12 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   constexpr int kChunkBytes = 128 * BITS / 8; // one row's codes per chunk
   constexpr int kGpc = 128 / GS;              // groups per chunk (1 or 2)
 
-  const int wave = int(threadIdx.x) >> 6;
+  // The wave index, and everything derived from it (tile, K range, chunk
+  // offsets), is uniform across the wave: readfirstlane tells the compiler,
+  // so the chunk offsets go to the loads' scalar offset.  (Derived from
+  // threadIdx.x alone it counts as divergent, and every buffer load with
+  // such a scalar offset becomes a loop over the distinct values.)
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int lane = int(threadIdx.x) & 63;
   const int ln = lane & 15;
   const int lh = lane >> 4;
@@ -196,59 +201,102 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     }
   };
 
-  // 1. Staging.  The wave's own staging loads (scale/bias pairs of its 16
-  //    rows and groups; kXWave: its slice of x) go out first, then the first
-  //    chunks' code loads, then the staging is stored: the wait for the
-  //    staging does not include the codes (the load counter retires in issue
-  //    order), which keep streaming.
+  // 1. Staging.  The wave's own staging loads go out first -- kXWave: its
+  //    slice of x (rows m < M only); then the scale/bias pairs of its 16 rows
+  //    and groups, as 16-byte pieces where the rows allow -- then the first
+  //    chunks' code loads; then the staging is stored.  The load counter
+  //    retires in issue order, so the waits for the staging do not include
+  //    the codes, which keep streaming.  Few load instructions go out before
+  //    the codes: the memory pipeline's cost is per instruction, not per byte.
   Chunk<BITS, MB, kXD> ring[DEPTH];
   {
-    // Lane (r, p) = (lane % 16, lane / 16) takes groups g0 + p + 4i of row
-    // r: each load instruction reads 16 rows x 4 consecutive groups.
-    constexpr int kSbIter = 4; // 16 groups per row per batch
     const int srow = min(int(blockIdx.x) * T * 16 + tl * 16 + ln, N - 1);
     const uint32_t sbase = uint32_t(int64_t(srow) * groups * sizeof(ST));
+    const uint32_t soff0 = uint32_t(g0) * uint32_t(sizeof(ST));
     constexpr int kXIter = kXWaveMaxChunks * 16 / 64; // x pieces per lane and row (kXWave)
     u32x4 xv[XM == kXWave ? 4 : 1][kXIter];
-    for (int gb = 0; gb < gw || gb == 0; gb += 4 * kSbIter) {
-      float sv[kSbIter], bv[kSbIter];
+    if constexpr (XM == kXWave) {
+      // Rows m < M (M <= 4) of columns [128 c0, 128 c1), eight per piece.
 #pragma unroll
-      for (int i = 0; i < kSbIter; ++i) {
-        const int g = gb + lh + 4 * i;
-        const uint32_t off = g < gw ? uint32_t(g0 + g) * uint32_t(sizeof(ST)) : kOob;
-        sv[i] = BLoadScalar<SDT>::get(rs_, sbase, off);
-        bv[i] = BLoadScalar<SDT>::get(rb_, sbase, off);
-      }
-      if (gb == 0) {
-        if constexpr (XM == kXWave) {
-          // Rows m < M (M <= 4) of columns [128 c0, 128 c1), eight per piece.
+      for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
 #pragma unroll
-          for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < kXIter; ++j) {
-              const int pc = lane + 64 * j;
-              const bool in = m < M && pc < ncs * 16;
-              const uint32_t off = in ? uint32_t((int64_t(m) * ldx + c0 * 128 + 8 * pc) * sizeof(XT)) : kOob;
-              xv[m][j] = BLoad8<XDT>::get(rx, off, 0);
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
-        if constexpr (XM == kXWave) {
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < kXIter; ++j) {
-              const int pc = lane + 64 * j;
-              if (m < M && pc < ncs * 16)
-                *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * pc) = xv[m][j];
-            }
+        for (int j = 0; j < kXIter; ++j) {
+          const int pc = lane + 64 * j;
+          const uint32_t off = pc < ncs * 16 ? uint32_t((int64_t(m) * ldx + c0 * 128 + 8 * pc) * sizeof(XT)) : kOob;
+          xv[m][j] = BLoad8<XDT>::get(rx, off, 0);
         }
       }
+    }
+    // Scale and bias pieces.  Vector form (rows and the wave's first group
+    // 16-byte aligned): lane (r, p) loads groups [kE p, kE p + kE) of row r
+    // (plus 4 kE per further batch), kE = 16 / sizeof(ST), so one
+    // instruction covers 16 rows x 4 kE groups.  Scalar form: one group per
+    // lane, groups p + 4i.  Lanes past the range read zeros.
+    constexpr int kE = 16 / int(sizeof(ST));
+    const bool vec_sb = (groups * int(sizeof(ST))) % 16 == 0 && soff0 % 16 == 0;
+    const int nbatch = vec_sb ? (gw + 4 * kE - 1) / (4 * kE) : (gw + 15) / 16;
+    constexpr int kMaxBatch = 2; // loads held in registers before the codes (more: second pass below)
+    u32x4 sq[kMaxBatch], bq[kMaxBatch];
+    if (vec_sb) {
 #pragma unroll
-      for (int i = 0; i < kSbIter; ++i) {
-        const int g = gb + lh + 4 * i;
-        if (g < gw) sbw[ln * L.gw + g] = make_float2(sv[i], fmaf(-kOff, sv[i], bv[i]));
+      for (int bt = 0; bt < kMaxBatch; ++bt) {
+        if (bt >= nbatch) break;
+        const int g = bt * 4 * kE + kE * lh;
+        const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
+        sq[bt] = bload16(rs_, voff, soff0);
+        bq[bt] = bload16(rb_, voff, soff0);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XM == kXWave) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
+#pragma unroll
+        for (int j = 0; j < kXIter; ++j) {
+          const int pc = lane + 64 * j;
+          if (pc < ncs * 16) *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * pc) = xv[m][j];
+        }
+      }
+    }
+    auto put = [&](int g, float sc, float bi) {
+      if (g < gw) sbw[ln * L.gw + g] = make_float2(sc, fmaf(-kOff, sc, bi));
+    };
+    auto pick_e = [&](const u32x4 &v, int e) -> float {
+      if constexpr (sizeof(ST) == 4) {
+        return __uint_as_float(v[e]);
+      } else {
+        const uint32_t wv = v[e >> 1];
+        return Elem<SDT>::load(typename Elem<SDT>::T((e & 1) ? (wv >> 16) : (wv & 0xffffu)));
+      }
+    };
+    if (vec_sb) {
+#pragma unroll
+      for (int bt = 0; bt < kMaxBatch; ++bt) {
+        if (bt >= nbatch) break;
+#pragma unroll
+        for (int e = 0; e < kE; ++e) put(bt * 4 * kE + kE * lh + e, pick_e(sq[bt], e), pick_e(bq[bt], e));
+      }
+      // Further batches (long K ranges): loaded and stored one at a time.
+      for (int bt = kMaxBatch; bt < nbatch; ++bt) {
+        const int g = bt * 4 * kE + kE * lh;
+        const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
+        const u32x4 a = bload16(rs_, voff, soff0), b = bload16(rb_, voff, soff0);
+#pragma unroll
+        for (int e = 0; e < kE; ++e) put(g + e, pick_e(a, e), pick_e(b, e));
+      }
+    } else {
+      // Unaligned rows: one group per lane, issued after the codes.
+      for (int gb = 0; gb < gw; gb += 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = gb + lh + 4 * i;
+          const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
+          put(g, BLoadScalar<SDT>::get(rs_, voff, soff0), BLoadScalar<SDT>::get(rb_, voff, soff0));
+        }
       }
     }
     if constexpr (XM == kXBlock) {

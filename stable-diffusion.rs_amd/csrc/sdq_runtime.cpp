@@ -326,7 +326,10 @@ struct WorkspaceSlot {
 };
 
 std::mutex g_ws_mu;
-std::map<WorkspaceKey, WorkspaceSlot> g_ws;
+// Never destroyed, like the pool: a static map's destructor would free its
+// buffers (HIP event records) during process teardown, after the HIP runtime
+// and any attached profiler have shut down.
+std::map<WorkspaceKey, WorkspaceSlot> &g_ws = *new std::map<WorkspaceKey, WorkspaceSlot>();
 
 WorkspaceKey ws_key(int device, hipStream_t stream) {
   WorkspaceKey k{device, stream, std::thread::id()};
