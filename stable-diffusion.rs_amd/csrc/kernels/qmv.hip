@@ -107,6 +107,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
       N * (K / group_size) * int64_t(dtype_size(s_dtype)) >= lim)
     fail("qmv: x, the packed weight, scales and biases must each be under 2 GiB");
   if (plan.row_blocks != (M <= 16 ? 1 : 2)) fail("qmv: plan's row blocks do not cover M");
+  if ((K / 128 + 1) * int64_t(plan.waves + 1) >= lim) fail("qmv: K too large for the chunk arithmetic");
   using namespace qmv_detail;
   if (plan.xmode < kXDirect || plan.xmode > kXBlock || plan.tiles_per_block < 1 || plan.waves < 1 ||
       plan.tiles_per_block * plan.waves > kMaxWaves[plan.xmode] ||

@@ -92,6 +92,32 @@ __device__ __forceinline__ u32x4 codes4_b(uint32_t wd) {
   return r;
 }
 
+// The same eight codes without the interleave: bf16 pairs (c0, c2), (c4, c6),
+// (c1, c3), (c5, c7) -- K slots in the order x_perm8 gives the activations.
+__device__ __forceinline__ u32x4 codes4_b_split(uint32_t wd) {
+  const uint32_t lo = wd & 0x0F0F0F0Fu;        // c0 c2 c4 c6
+  const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu; // c1 c3 c5 c7
+  const uint32_t k43 = 0x43434343u;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(k43, lo, 0x04010400u); // (c0, c2)
+  r[1] = __builtin_amdgcn_perm(k43, lo, 0x04030402u); // (c4, c6)
+  r[2] = __builtin_amdgcn_perm(k43, hi, 0x04010400u); // (c1, c3)
+  r[3] = __builtin_amdgcn_perm(k43, hi, 0x04030402u); // (c5, c7)
+  return r;
+}
+
+// Eight activations (bf16 pairs (x0, x1) .. (x6, x7)) reordered to the K
+// slots of codes4_b_split: (x0, x2), (x4, x6), (x1, x3), (x5, x7).  Applied
+// once when x is staged, it saves two permutes per code word in the stream.
+__device__ __forceinline__ u32x4 x_perm8(const u32x4 &v) {
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+  r[2] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
+  r[3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
+  return r;
+}
+
 // Eight 8-bit codes (two words), in element order, as exact bf16 values q.
 __device__ __forceinline__ u32x4 codes8_b(uint32_t w0, uint32_t w1) {
   const uint32_t a = opaque(w0), b = opaque(w1);
@@ -156,8 +182,9 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   // This wave's chunks [c0, c1) of the 128-wide chunks and groups [g0, g1);
   // the last chunk is half when K % 128 == 64 (group size 64).
   const int nchunk = (K + 127) / 128;
-  const int c0 = int((int64_t(nchunk) * rs) / S);
-  const int c1 = int((int64_t(nchunk) * (rs + 1)) / S);
+  // 32-bit products: nchunk * S < 2^31 (checked on the host).
+  const int c0 = int(uint32_t(nchunk * rs) / uint32_t(S));
+  const int c1 = int(uint32_t(nchunk * (rs + 1)) / uint32_t(S));
   const int ncs = live ? c1 - c0 : 0;
   const bool half_tail = (K & 127) != 0;
   const int g0 = c0 * kGpc;
@@ -201,67 +228,24 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     }
   };
 
-  // 1. Staging.  The wave's own staging loads go out first -- kXWave: its
-  //    slice of x (rows m < M only); then the scale/bias pairs of its 16 rows
-  //    and groups, as 16-byte pieces where the rows allow -- then the first
-  //    chunks' code loads; then the staging is stored.  The load counter
-  //    retires in issue order, so the waits for the staging do not include
-  //    the codes, which keep streaming.  Few load instructions go out before
-  //    the codes: the memory pipeline's cost is per instruction, not per byte.
-  Chunk<BITS, MB, kXD> ring[DEPTH];
+  // 1. Staging.  Order matters, for two reasons.
+  //    * The load counter retires in issue order: staging loads (x, the
+  //      scale/bias pairs) go out before the code loads, so the waits for the
+  //      staging do not include the codes, which keep streaming.
+  //    * The compiler counts the loads in flight per register.  A load under
+  //      a branch issued between a code load and its use makes it assume the
+  //      worst and wait for every load.  So everything conditional (rows
+  //      m < M, the scale form, long ranges) comes first, then the code
+  //      loads, unconditionally, then the stores of the staged values.
+  //    Few load instructions go out before the codes: the memory pipeline's
+  //    cost is per instruction, not per byte.
+  // Staged 4-bit: x is stored in the K-slot order of codes4_b_split.
+  constexpr bool kXPerm = BITS == 4 && !kXD;
+  Chunk<BITS, MB, kXD> ring[DEPTH + 1];
   {
     const int srow = min(int(blockIdx.x) * T * 16 + tl * 16 + ln, N - 1);
     const uint32_t sbase = uint32_t(int64_t(srow) * groups * sizeof(ST));
     const uint32_t soff0 = uint32_t(g0) * uint32_t(sizeof(ST));
-    constexpr int kXIter = kXWaveMaxChunks * 16 / 64; // x pieces per lane and row (kXWave)
-    u32x4 xv[XM == kXWave ? 4 : 1][kXIter];
-    if constexpr (XM == kXWave) {
-      // Rows m < M (M <= 4) of columns [128 c0, 128 c1), eight per piece.
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m >= M) break;
-#pragma unroll
-        for (int j = 0; j < kXIter; ++j) {
-          const int pc = lane + 64 * j;
-          const uint32_t off = pc < ncs * 16 ? uint32_t((int64_t(m) * ldx + c0 * 128 + 8 * pc) * sizeof(XT)) : kOob;
-          xv[m][j] = BLoad8<XDT>::get(rx, off, 0);
-        }
-      }
-    }
-    // Scale and bias pieces.  Vector form (rows and the wave's first group
-    // 16-byte aligned): lane (r, p) loads groups [kE p, kE p + kE) of row r
-    // (plus 4 kE per further batch), kE = 16 / sizeof(ST), so one
-    // instruction covers 16 rows x 4 kE groups.  Scalar form: one group per
-    // lane, groups p + 4i.  Lanes past the range read zeros.
-    constexpr int kE = 16 / int(sizeof(ST));
-    const bool vec_sb = (groups * int(sizeof(ST))) % 16 == 0 && soff0 % 16 == 0;
-    const int nbatch = vec_sb ? (gw + 4 * kE - 1) / (4 * kE) : (gw + 15) / 16;
-    constexpr int kMaxBatch = 2; // loads held in registers before the codes (more: second pass below)
-    u32x4 sq[kMaxBatch], bq[kMaxBatch];
-    if (vec_sb) {
-#pragma unroll
-      for (int bt = 0; bt < kMaxBatch; ++bt) {
-        if (bt >= nbatch) break;
-        const int g = bt * 4 * kE + kE * lh;
-        const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
-        sq[bt] = bload16(rs_, voff, soff0);
-        bq[bt] = bload16(rb_, voff, soff0);
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (XM == kXWave) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m >= M) break;
-#pragma unroll
-        for (int j = 0; j < kXIter; ++j) {
-          const int pc = lane + 64 * j;
-          if (pc < ncs * 16) *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * pc) = xv[m][j];
-        }
-      }
-    }
     auto put = [&](int g, float sc, float bi) {
       if (g < gw) sbw[ln * L.gw + g] = make_float2(sc, fmaf(-kOff, sc, bi));
     };
@@ -273,65 +257,149 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
         return Elem<SDT>::load(typename Elem<SDT>::T((e & 1) ? (wv >> 16) : (wv & 0xffffu)));
       }
     };
+
+    // (a) kXBlock: the block stages all of x, eight values per piece, for
+    //     its T tiles.  The first round of loads is held in registers and
+    //     stored after the code loads; further rounds (large x) are loaded
+    //     and stored here.
+    constexpr int kXLoads = 8;
+    const int tid = int(threadIdx.x);
+    const int nthreads = int(blockDim.x);
+    const int per_row = K / 8;
+    const int x_pieces = M * per_row;
+    // Row of piece e: a float estimate corrected once (exact: the estimate
+    // is off by at most one for these sizes).
+    const float inv_per_row = 1.0f / float(per_row);
+    auto x_row = [&](int e) {
+      int m = int(float(e) * inv_per_row);
+      m -= m * per_row > e;
+      m += (m + 1) * per_row <= e;
+      return m;
+    };
+    auto xb_load = [&](int base, u32x4 (&v)[kXLoads]) {
+#pragma unroll
+      for (int j = 0; j < kXLoads; ++j) {
+        const int e = min(base + j * nthreads + tid, x_pieces - 1);
+        const int m = x_row(e);
+        v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + 8 * (e - m * per_row));
+      }
+    };
+    auto xb_store = [&](int base, const u32x4 (&v)[kXLoads]) {
+#pragma unroll
+      for (int j = 0; j < kXLoads; ++j) {
+        const int e = base + j * nthreads + tid;
+        if (e < x_pieces) {
+          const int m = x_row(e);
+          *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * (e - m * per_row)) = kXPerm ? x_perm8(v[j]) : v[j];
+        }
+      }
+    };
+    u32x4 xb[XM == kXBlock ? kXLoads : 1];
+    if constexpr (XM == kXBlock) {
+      for (int base = kXLoads * nthreads; base < x_pieces; base += kXLoads * nthreads) {
+        u32x4 v[kXLoads];
+        xb_load(base, v);
+        xb_store(base, v);
+      }
+      xb_load(0, xb);
+    }
+
+    // (b) kXWave: the wave's slice of x, rows m < M (M <= 4) of columns
+    //     [128 c0, 128 c1), eight per piece.
+    constexpr int kXIter = kXWaveMaxChunks * 16 / 64; // x pieces per lane and row
+    u32x4 xv[XM == kXWave ? 4 : 1][kXIter];
+    if constexpr (XM == kXWave) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
+#pragma unroll
+        for (int j = 0; j < kXIter; ++j) {
+          const int pc = lane + 64 * j;
+          const uint32_t off = pc < ncs * 16 ? uint32_t((int64_t(m) * ldx + c0 * 128 + 8 * pc) * sizeof(XT)) : kOob;
+          xv[m][j] = BLoad8<XDT>::get(rx, off, 0);
+        }
+      }
+    }
+
+    // (c) Scale and bias pieces.  Vector form (rows and the wave's first
+    //     group 16-byte aligned): lane (r, p) loads groups [kE p, kE p + kE)
+    //     of row r (plus 4 kE per further batch), kE = 16 / sizeof(ST), so
+    //     one instruction covers 16 rows x 4 kE groups.  Scalar form: one
+    //     group per lane, groups p + 4i.  Lanes past the range read zeros.
+    //     The first kMaxBatch batches (16 groups in scalar form) are held in
+    //     registers and stored after the code loads; further ones (long
+    //     ranges) are loaded and stored here.
+    constexpr int kE = 16 / int(sizeof(ST));
+    constexpr int kMaxBatch = 2;
+    const bool vec_sb = (groups * int(sizeof(ST))) % 16 == 0 && soff0 % 16 == 0;
+    const int nbatch = vec_sb ? (gw + 4 * kE - 1) / (4 * kE) : (gw + 15) / 16;
+    auto sb_off = [&](int g) { return g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob; };
+    u32x4 sq[kMaxBatch], bq[kMaxBatch];
+    float sv[4], bv[4];
     if (vec_sb) {
+      for (int bt = kMaxBatch; bt < nbatch; ++bt) {
+        const int g = bt * 4 * kE + kE * lh;
+        const u32x4 a = bload16(rs_, sb_off(g), soff0), b = bload16(rb_, sb_off(g), soff0);
+#pragma unroll
+        for (int e = 0; e < kE; ++e) put(g + e, pick_e(a, e), pick_e(b, e));
+      }
+#pragma unroll
+      for (int bt = 0; bt < kMaxBatch; ++bt) {
+        if (bt >= nbatch) break;
+        const int g = bt * 4 * kE + kE * lh;
+        sq[bt] = bload16(rs_, sb_off(g), soff0);
+        bq[bt] = bload16(rb_, sb_off(g), soff0);
+      }
+    } else {
+      for (int gb = 16; gb < gw; gb += 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = gb + lh + 4 * i;
+          put(g, BLoadScalar<SDT>::get(rs_, sb_off(g), soff0), BLoadScalar<SDT>::get(rb_, sb_off(g), soff0));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[i] = BLoadScalar<SDT>::get(rs_, sb_off(lh + 4 * i), soff0);
+        bv[i] = BLoadScalar<SDT>::get(rb_, sb_off(lh + 4 * i), soff0);
+      }
+    }
+
+    // (d) The code loads of the first DEPTH chunks, unconditionally.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (e) Stores of the staged values.  The scale form is re-read through an
+    //     opaque copy, so the compiler cannot merge this branch with (c) and
+    //     move these stores (and their waits) above the code loads.
+    if constexpr (XM == kXBlock) xb_store(0, xb);
+    if constexpr (XM == kXWave) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
+#pragma unroll
+        for (int j = 0; j < kXIter; ++j) {
+          const int pc = lane + 64 * j;
+          if (pc < ncs * 16) *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * pc) = kXPerm ? x_perm8(xv[m][j]) : xv[m][j];
+        }
+      }
+    }
+    int vec2 = __builtin_amdgcn_readfirstlane(int(vec_sb));
+    asm volatile("" : "+s"(vec2));
+    if (vec2) {
 #pragma unroll
       for (int bt = 0; bt < kMaxBatch; ++bt) {
         if (bt >= nbatch) break;
 #pragma unroll
         for (int e = 0; e < kE; ++e) put(bt * 4 * kE + kE * lh + e, pick_e(sq[bt], e), pick_e(bq[bt], e));
       }
-      // Further batches (long K ranges): loaded and stored one at a time.
-      for (int bt = kMaxBatch; bt < nbatch; ++bt) {
-        const int g = bt * 4 * kE + kE * lh;
-        const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
-        const u32x4 a = bload16(rs_, voff, soff0), b = bload16(rb_, voff, soff0);
-#pragma unroll
-        for (int e = 0; e < kE; ++e) put(g + e, pick_e(a, e), pick_e(b, e));
-      }
     } else {
-      // Unaligned rows: one group per lane, issued after the codes.
-      for (int gb = 0; gb < gw; gb += 16) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int g = gb + lh + 4 * i;
-          const uint32_t voff = g < gw ? sbase + uint32_t(g) * uint32_t(sizeof(ST)) : kOob;
-          put(g, BLoadScalar<SDT>::get(rs_, voff, soff0), BLoadScalar<SDT>::get(rb_, voff, soff0));
-        }
-      }
+      for (int i = 0; i < 4; ++i) put(lh + 4 * i, sv[i], bv[i]);
     }
     if constexpr (XM == kXBlock) {
-      // The block stages all of x, eight values per piece, for its T tiles.
-      constexpr int kXLoads = 8;
-      const int nthreads = int(blockDim.x);
-      const int tid = int(threadIdx.x);
-      const int per_row = K / 8;
-      const int x_pieces = M * per_row;
-      // Row of piece e: a float estimate corrected once (exact: the
-      // estimate is off by at most one for these sizes).
-      const float inv_per_row = 1.0f / float(per_row);
-      auto x_row = [&](int e) {
-        int m = int(float(e) * inv_per_row);
-        m -= m * per_row > e;
-        m += (m + 1) * per_row <= e;
-        return m;
-      };
-      for (int base = 0; base < x_pieces; base += kXLoads * nthreads) {
-        u32x4 v[kXLoads];
-#pragma unroll
-        for (int j = 0; j < kXLoads; ++j) {
-          const int e = min(base + j * nthreads + tid, x_pieces - 1);
-          const int m = x_row(e);
-          v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + 8 * (e - m * per_row));
-        }
-#pragma unroll
-        for (int j = 0; j < kXLoads; ++j) {
-          const int e = base + j * nthreads + tid;
-          if (e < x_pieces) {
-            const int m = x_row(e);
-            *reinterpret_cast<u32x4 *>(xl + m * L.xstride + 8 * (e - m * per_row)) = v[j];
-          }
-        }
-      }
       __syncthreads();
     } else {
       // The stage is this wave's own: a wave-scope fence orders it.
@@ -351,64 +419,97 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   // Column of chunk c's K range within the staged x rows.
   const int xcol0 = XM == kXBlock ? 0 : c0 * 128;
 
-  for (int base = 0; base < ncs; base += DEPTH) {
+  // One chunk's math: chunk i (local) of the range, codes in q.
+  auto process = [&](const int i, const Chunk<BITS, MB, kXD> &q) __attribute__((always_inline)) {
+    const int c = c0 + i;
+    u32x4 bq[4];
+    if constexpr (BITS == 4) {
+      uint32_t w0 = q.q[0][0], w1 = q.q[0][1], w2 = q.q[0][2], w3 = q.q[0][3];
+      perm32_swap(w0, w2);
+      perm32_swap(w1, w3);
+      perm16_swap(w0, w1);
+      perm16_swap(w2, w3);
+      if constexpr (kXPerm) {
+        bq[0] = codes4_b_split(w0);
+        bq[1] = codes4_b_split(w1);
+        bq[2] = codes4_b_split(w2);
+        bq[3] = codes4_b_split(w3);
+      } else {
+        bq[0] = codes4_b(w0);
+        bq[1] = codes4_b(w1);
+        bq[2] = codes4_b(w2);
+        bq[3] = codes4_b(w3);
+      }
+    } else {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int i = base + d;
-      Chunk<BITS, MB, kXD> &q = ring[d];
-      if (i < ncs) {
-        const int c = c0 + i;
-        u32x4 bq[4];
-        if constexpr (BITS == 4) {
-          uint32_t w0 = q.q[0][0], w1 = q.q[0][1], w2 = q.q[0][2], w3 = q.q[0][3];
-          perm32_swap(w0, w2);
-          perm32_swap(w1, w3);
-          perm16_swap(w0, w1);
-          perm16_swap(w2, w3);
-          bq[0] = codes4_b(w0);
-          bq[1] = codes4_b(w1);
-          bq[2] = codes4_b(w2);
-          bq[3] = codes4_b(w3);
-        } else {
+      for (int j = 0; j < 4; ++j) bq[j] = codes8_b(q.q[j >> 1][2 * (j & 1)], q.q[j >> 1][2 * (j & 1) + 1]);
+    }
+    // The chunk's MFMAs, group by group: t = sum x c, xs = sum x.
+    const bool two = !(half_tail && c == nchunk - 1); // second half of the chunk exists
 #pragma unroll
-          for (int j = 0; j < 4; ++j) bq[j] = codes8_b(q.q[j >> 1][2 * (j & 1)], q.q[j >> 1][2 * (j & 1) + 1]);
-        }
-        // The chunk's MFMAs, group by group: t = sum x c, xs = sum x.
-        const bool two = !(half_tail && c == nchunk - 1); // second half of the chunk exists
+    for (int gg = 0; gg < kGpc; ++gg) {
+      if (gg == 1 && !two) break;
+      constexpr int kPer = 4 / kGpc; // MFMAs per group in this chunk
+      floatx4 t[MB], xs[MB];
 #pragma unroll
-        for (int gg = 0; gg < kGpc; ++gg) {
-          if (gg == 1 && !two) break;
-          constexpr int kPer = 4 / kGpc; // MFMAs per group in this chunk
-          floatx4 t[MB], xs[MB];
+      for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-              const int mi = gg * kPer + j;
-              u32x4 a;
-              if constexpr (kXD) {
-                a = q.a[mb][mi];
-              } else {
-                a = *reinterpret_cast<const u32x4 *>(xl + xrow[mb] * L.xstride + c * 128 - xcol0 +
-                                                     slot_k<BITS>(mi, lh));
-              }
-              t[mb] = mfma16(a, bq[mi], j == 0 ? zero : t[mb]);
-              xs[mb] = mfma16(a, ones, j == 0 ? zero : xs[mb]);
-            }
+        for (int j = 0; j < kPer; ++j) {
+          const int mi = gg * kPer + j;
+          u32x4 a;
+          if constexpr (kXD) {
+            a = q.a[mb][mi];
+          } else {
+            a = *reinterpret_cast<const u32x4 *>(xl + xrow[mb] * L.xstride + c * 128 - xcol0 +
+                                                 slot_k<BITS>(mi, lh));
           }
-          const float2 sc = sbrow[i * kGpc + gg];
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              acc[mb][e] = fmaf(sc.x, t[mb][e], acc[mb][e]);
-              acc[mb][e] = fmaf(sc.y, xs[mb][e], acc[mb][e]);
-            }
+          t[mb] = mfma16(a, bq[mi], j == 0 ? zero : t[mb]);
+          xs[mb] = mfma16(a, ones, j == 0 ? zero : xs[mb]);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-      load(i + DEPTH, q);
-      __builtin_amdgcn_sched_barrier(0);
+      const float2 sc = sbrow[i * kGpc + gg];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // Entry e of lane (n, h) is token 16 mb + 4 h + e: for M <= 4 only
+          // e < M holds a token on any lane (a uniform test).
+          if (M > 4 || e < M) {
+            acc[mb][e] = fmaf(sc.x, t[mb][e], acc[mb][e]);
+            acc[mb][e] = fmaf(sc.y, xs[mb][e], acc[mb][e]);
+          }
+        }
+    }
+  };
+  {
+    // Ring of DEPTH + 1 slots: the load of chunk i + DEPTH goes out before
+    // chunk i is processed (into the slot chunk i - 1 left), so the math of
+    // a chunk does not delay the stream.  Every load is unconditional (past
+    // the range it reads zeros without touching memory): the compiler then
+    // counts the loads in flight exactly and each chunk waits only for its
+    // own; a load under a branch would make it wait for all of them.
+    // Ranges of up to kStraight chunks run as straight-line code: at a loop
+    // header the compiler merges the states of entry and back edge and waits
+    // for every load in flight.
+    constexpr int kRing = DEPTH + 1;
+    constexpr int kStraight = 8;
+    if (ncs <= kStraight) {
+#pragma unroll
+      for (int i = 0; i < kStraight; ++i) {
+        if (i >= ncs) break;
+        load(i + DEPTH, ring[(i + DEPTH) % kRing]);
+        process(i, ring[i % kRing]);
+      }
+    } else {
+      for (int base = 0; base < ncs; base += kRing) {
+#pragma unroll
+        for (int d = 0; d < kRing; ++d) {
+          const int i = base + d;
+          if (i >= ncs) break;
+          load(i + DEPTH, ring[(d + DEPTH) % kRing]);
+          process(i, ring[d]);
+        }
+      }
     }
   }
 
