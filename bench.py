@@ -146,8 +146,8 @@ def parse():
                     help="comma-separated M values of the 3072->12288 sweep")
     ap.add_argument("--sweep-bits", default="4,8", help="comma-separated bit widths of the sweep")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="after the timed steps, run one f32->bf16 copy of 2^27 elements (512 MiB read, "
-                         "256 MiB written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
+                    help="at the end, run one f32->bf16 copy of 2^27 elements (512 MiB read, 256 MiB "
+                         "written): the known-size kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -387,13 +387,6 @@ def main():
         for i in range(args.steps):
             step(i, head_fused, evs[i])
         torch.cuda.synchronize()
-        if args.copy_probe:
-            src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
-            dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
-            torch.cuda.synchronize()
-            dst.copy_(src)
-            torch.cuda.synchronize()
-            del src, dst
         k_fc1 = float(np.median([e[0].elapsed_time(e[1]) for e in evs]))
         k_gelu = float(np.median([e[1].elapsed_time(e[2]) for e in evs]))
         k_fc2 = float(np.median([e[2].elapsed_time(e[3]) for e in evs]))
@@ -501,6 +494,14 @@ def main():
                            "(residual writers 8-bit), reference_mixed4 = quantized.rs:156-166",
                    **per_policy}
         del xs, ys
+
+    if args.copy_probe:
+        src = torch.zeros(1 << 27, device=dev, dtype=torch.float32)
+        dst = torch.empty(1 << 27, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if do_step and not args.no_cpu_baseline:

@@ -206,6 +206,9 @@ __device__ __forceinline__ float gelu_approx_f(float v) {
   return u >= 0.0f ? v * (1.0f - r) : v * r;
 }
 
+// Bytes per element of a float dtype code.
+__device__ __forceinline__ int dtype_size_dev(int dt) { return dt == SDQ_FLOAT32 ? 4 : 2; }
+
 // One value of a float32/bfloat16/float16 array as f32.
 __device__ __forceinline__ float epi_load(const void *p, int dtype, int64_t i) {
   if (dtype == SDQ_FLOAT32) return static_cast<const float *>(p)[i];
@@ -231,6 +234,68 @@ __device__ __forceinline__ float epi_combine(const kern::Epilogue &ep, float v, 
   if (ep.combine == 2) return v * r;
   const float g = ep.gate ? epi_load(ep.gate, ep.gate_dtype, n) : 1.0f;
   return fmaf(g, v, r);
+}
+
+// n consecutive values (n = 4 or 8) of a float32/bfloat16/float16 array at
+// element i as f32; one or two 16-byte loads when `vec` (the caller has
+// checked the alignment), single elements otherwise.
+template <int NV>
+__device__ __forceinline__ void epi_loadn(const void *p, int dtype, int64_t i, bool vec, float (&out)[NV]) {
+  static_assert(NV == 4 || NV == 8, "4 or 8 values");
+  if (!vec) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) out[k] = epi_load(p, dtype, i + k);
+    return;
+  }
+  if (dtype == SDQ_FLOAT32) {
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(static_cast<const float *>(p) + i);
+#pragma unroll
+    for (int h = 0; h < NV / 4; ++h) {
+      const u32x4 a = q[h];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[4 * h + k] = __uint_as_float(a[k]);
+    }
+  } else {
+    const uint16_t *base = static_cast<const uint16_t *>(p) + i;
+    uint32_t w[NV / 2];
+    if constexpr (NV == 8) {
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(base);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = a[k];
+    } else {
+      const u32x2 a = *reinterpret_cast<const u32x2 *>(base);
+      w[0] = a[0];
+      w[1] = a[1];
+    }
+#pragma unroll
+    for (int k = 0; k < NV / 2; ++k) {
+      out[2 * k] = dtype == SDQ_BFLOAT16 ? bf16_bits_to_f32(w[k] & 0xffffu) : f16_bits_to_f32(w[k] & 0xffffu);
+      out[2 * k + 1] = dtype == SDQ_BFLOAT16 ? bf16_bits_to_f32(w[k] >> 16) : f16_bits_to_f32(w[k] >> 16);
+    }
+  }
+}
+
+// The combine stage on NV consecutive outputs (m, n .. n + NV - 1), each
+// already rounded to the output dtype (as the unfused sequence rounds the
+// linear's result): y = r + g * v with one fused multiply-add, or v * r.
+// `vec`: residual row and gate 16-byte aligned at n (checked by the caller).
+template <int NV>
+__device__ __forceinline__ void epi_combine_n(const kern::Epilogue &ep, int64_t m, int64_t n, bool vec,
+                                              float (&v)[NV]) {
+  float r[NV];
+  epi_loadn<NV>(ep.res, ep.res_dtype, m * ep.ld_res + n, vec, r);
+  if (ep.combine == 2) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] *= r[k];
+  } else if (!ep.gate) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] += r[k];
+  } else {
+    float g[NV];
+    epi_loadn<NV>(ep.gate, ep.gate_dtype, n, vec, g);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = fmaf(g[k], v[k], r[k]);
+  }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {

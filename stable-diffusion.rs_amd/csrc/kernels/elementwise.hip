@@ -87,93 +87,6 @@ __global__ __launch_bounds__(kThreads) void gelu_kernel(const typename Elem<D>::
     out[i] = Elem<D>::store(gelu_approx_f(Elem<D>::load(a[i])));
 }
 
-// Eight consecutive elements of a float32/bfloat16/float16 array as f32,
-// and back: 16-byte accesses (two for f32); `p` must be 16-byte aligned.
-template <int D>
-__device__ __forceinline__ void load8f(const typename Elem<D>::T *p, float (&v)[8]) {
-  if constexpr (sizeof(typename Elem<D>::T) == 4) {
-    const u32x4 a = reinterpret_cast<const u32x4 *>(p)[0];
-    const u32x4 b = reinterpret_cast<const u32x4 *>(p)[1];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[k] = __uint_as_float(a[k]);
-      v[4 + k] = __uint_as_float(b[k]);
-    }
-  } else {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(p);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[2 * k] = Elem<D>::load(typename Elem<D>::T(a[k] & 0xffffu));
-      v[2 * k + 1] = Elem<D>::load(typename Elem<D>::T(a[k] >> 16));
-    }
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void store8f(typename Elem<D>::T *p, const float (&v)[8]) {
-  if constexpr (sizeof(typename Elem<D>::T) == 4) {
-    u32x4 a, b;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      a[k] = __float_as_uint(v[k]);
-      b[k] = __float_as_uint(v[4 + k]);
-    }
-    reinterpret_cast<u32x4 *>(p)[0] = a;
-    reinterpret_cast<u32x4 *>(p)[1] = b;
-  } else {
-    u32x4 a;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      a[k] = uint32_t(Elem<D>::store(v[2 * k])) | (uint32_t(Elem<D>::store(v[2 * k + 1])) << 16);
-    *reinterpret_cast<u32x4 *>(p) = a;
-  }
-}
-
-// The epilogue's combine stage over a finished [M, N] output, in place:
-// y = r + g * y (COMB 1; G = 0: no gate) or y * r (COMB 2), r [M, N] with row
-// stride N.  Used after the large-M kernel, whose tile store does not carry
-// the combine stage.  Groups of eight consecutive elements of a row per
-// thread, every operand in 16-byte pieces; the host checks that rows are
-// whole groups and every pointer is 16-byte aligned.
-template <int D, int R, int G, int COMB>
-__global__ __launch_bounds__(kThreads) void combine8_kernel(typename Elem<D>::T *__restrict__ y,
-                                                            const typename Elem<R>::T *__restrict__ res,
-                                                            const void *__restrict__ gate,
-                                                            int64_t M, int64_t N) {
-  const int64_t stride = int64_t(gridDim.x) * kThreads;
-  const int64_t groups = M * N / 8;
-  for (int64_t g = int64_t(blockIdx.x) * kThreads + threadIdx.x; g < groups; g += stride) {
-    const int64_t e0 = g * 8;
-    float v[8], r[8];
-    load8f<D>(y + e0, v);
-    load8f<R>(res + e0, r);
-    if constexpr (COMB == 2) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] *= r[k];
-    } else if constexpr (G == 0) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] += r[k];
-    } else {
-      float gv[8];
-      load8f<G>(static_cast<const typename Elem<G>::T *>(gate) + (e0 % N), gv);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = fmaf(gv[k], v[k], r[k]);
-    }
-    store8f<D>(y + e0, v);
-  }
-}
-
-// Any shape or alignment: one element per thread.
-template <int D>
-__global__ __launch_bounds__(kThreads) void combine_kernel(typename Elem<D>::T *__restrict__ y,
-                                                           int64_t M, int64_t N,
-                                                           kern::Epilogue ep) {
-  const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < M * N; i += stride) {
-    const int64_t m = i / N, n = i - m * N;
-    y[i] = Elem<D>::store(epi_combine(ep, Elem<D>::load(y[i]), m, n));
-  }
-}
 
 #define SDQ_FLOAT_DISPATCH(dt, NAME, ...)                                    \
   switch (dt) {                                                              \
@@ -261,39 +174,6 @@ void gelu_approx(const void *a, int dtype, void *out, int64_t n,
   hip_check(hipGetLastError(), "gelu launch");
 }
 
-void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue &ep,
-                     hipStream_t stream) {
-  if (M == 0 || N == 0 || ep.combine == 0) return;
-  if (!epilogue_ok(ep)) fail("combine: bad epilogue");
-  const auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool vec = N % 8 == 0 && ep.ld_res == N && a16(y) && a16(ep.res) && (!ep.gate || a16(ep.gate));
-  if (!vec) {
-    const int grid = grid_for(M * N / 4 + 1);
-    SDQ_FLOAT_DISPATCH(y_dtype, D, {
-      combine_kernel<D><<<grid, kThreads, 0, stream>>>(static_cast<typename Elem<D>::T *>(y), M, N, ep);
-    });
-    hip_check(hipGetLastError(), "combine launch");
-    return;
-  }
-  const int grid = grid_for(M * N / 8 / 4 + 1);
-  const int gdt = ep.gate ? ep.gate_dtype : 0;
-  SDQ_FLOAT_DISPATCH(y_dtype, D, {
-    SDQ_FLOAT_DISPATCH(ep.res_dtype, R, {
-      auto *yp = static_cast<typename Elem<D>::T *>(y);
-      auto *rp = static_cast<const typename Elem<R>::T *>(ep.res);
-      if (ep.combine == 2) {
-        combine8_kernel<D, R, 0, 2><<<grid, kThreads, 0, stream>>>(yp, rp, nullptr, M, N);
-      } else if (gdt == 0) {
-        combine8_kernel<D, R, 0, 1><<<grid, kThreads, 0, stream>>>(yp, rp, nullptr, M, N);
-      } else {
-        SDQ_FLOAT_DISPATCH(gdt, G, {
-          combine8_kernel<D, R, G, 1><<<grid, kThreads, 0, stream>>>(yp, rp, ep.gate, M, N);
-        });
-      }
-    });
-  });
-  hip_check(hipGetLastError(), "combine launch");
-}
 
 void fill_zero(void *p, size_t bytes, hipStream_t stream) {
   const int64_t words = int64_t(bytes / 4);

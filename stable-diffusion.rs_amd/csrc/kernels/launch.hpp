@@ -48,9 +48,9 @@ void gguf_quantize(const uint8_t *raw, int type, int64_t rows, int64_t cols, int
 // the bias add (quantized.rs:314-317), the Flux MLP's GELU (flux.rs:400-413),
 // the gated residual x + gate * y (flux.rs:389-398, 414, 470) and T5's
 // gelu(wi_0 x) * (wi_1 x) (t5.rs:209-214).  The small-M kernel applies the
-// combine stage to the f32 value in its store; after the large-M kernel it
-// runs as one in-place pass over the output (combine_inplace), on the
-// rounded v, as the unfused sequence does.
+// combine stage to the f32 value in its store; the large-M kernel applies it
+// in its store (or its reduction kernel) to v rounded to the output dtype, as
+// the unfused sequence does.
 struct Epilogue {
   const void *bias = nullptr;
   int bias_dtype = 0;
@@ -115,6 +115,9 @@ struct QmmPlan {
   int steps_per_split = 0;  // 64-wide K steps per range
   int sk_workers = 0;       // > 0: stream-K over this many blocks (one per CU)
   int blocks = 0;           // grid size
+  int tiles_m = 0;          // tiles along M
+  int group_m = 1;          // tile order: groups of group_m tile rows, column by column
+  int xcds = 1;             // L2 domains the hardware deals blocks to, round robin
   size_t partial_floats = 0; // workspace needed (0 without split tiles)
 };
 
@@ -122,7 +125,7 @@ struct QmmPlan {
 // max_partial_floats caps the split-K workspace the plan may use (the
 // no-allocation entry point's fixed scratch); a split that would need more
 // is not taken.
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus,
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus,
                  size_t max_partial_floats = ~size_t(0), bool allow_stream_k = true);
 // Zeroes `bytes` (a multiple of 4) at `p` with a kernel on `stream`.
 void fill_zero(void *p, size_t bytes, hipStream_t stream);
@@ -207,10 +210,6 @@ void multiply(const void *a, int a_dtype, const void *b, int b_dtype,
               void *out, int out_dtype, int64_t n, hipStream_t stream);
 void gelu_approx(const void *a, int dtype, void *out, int64_t n,
                  hipStream_t stream);
-// The epilogue's combine stage (residual / gate / product) over a finished
-// y [M, N] in place; nothing when ep.combine == 0.
-void combine_inplace(void *y, int y_dtype, int64_t M, int64_t N, const Epilogue &ep,
-                     hipStream_t stream);
 
 // y [M, N] = a [M, K] @ b [N, K].T, f32 accumulate; y in the promotion of
 // the two dtypes.  dense.hip.

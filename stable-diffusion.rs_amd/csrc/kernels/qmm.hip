@@ -3,6 +3,7 @@
 // combination): the MFMA-bound side of mlx_quantized_matmul
 // (crates/sd-tensor/src/mlx.rs:386-397, 1947-1975).
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <string>
 
@@ -39,12 +40,13 @@ namespace {
 
 namespace kern {
 
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_floats,
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_partial_floats,
                  bool allow_stream_k) {
   QmmPlan p;
   p.bm = M <= 128 ? 128 : 256;
   p.tiles_n = int((N + qmm_detail::kTileN - 1) / qmm_detail::kTileN);
   const int64_t tiles_m = (M + p.bm - 1) / p.bm;
+  p.tiles_m = int(tiles_m);
   p.tiles = int(tiles_m * p.tiles_n);
   const int64_t steps = K / 64;
   const int64_t slots = cus > 0 ? cus : 256; // one block per CU at a time
@@ -112,6 +114,19 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int cus, size_t max_partial_fl
   const int64_t sk_tiles = p.tiles - p.dp_tiles;
   p.blocks = int(p.dp_tiles + sk_tiles * p.splits);
   p.partial_floats = size_t(sk_tiles) * size_t(p.splits) * tile_floats;
+  // Data-parallel launches run in XCD order (MI355X: 8 XCDs of 32 CUs, each
+  // with its own L2), each XCD taking a contiguous run of the tile order.
+  // The group height makes one XCD's run a near-square block of tiles,
+  // weighted by the bytes a tile row shares (its activation panel, BM rows)
+  // against a tile column (its weight panel, 256 rows of codes): rows / cols
+  // ~ weight bytes / activation bytes = bits / (8 * 2) * 256 / BM.
+  p.xcds = slots % 8 == 0 && slots >= 64 ? 8 : 1;
+  {
+    const double per_xcd = std::max(1.0, double(p.tiles) / p.xcds);
+    const double ratio = double(bits) / 16.0 * 256.0 / p.bm;
+    const int64_t gm = int64_t(std::lround(std::sqrt(per_xcd * ratio)));
+    p.group_m = int(std::clamp<int64_t>(gm, 1, tiles_m));
+  }
   return p;
 }
 
@@ -135,8 +150,9 @@ void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
     fail("qmm: x, the packed weight, scales and biases must each be under 2 GiB");
   // The launch must be exactly the plan for this shape: the grid, the
   // per-range K bounds and the workspace all follow from it.
-  const QmmPlan want = plan_qmm(M, N, K, 0);
-  if (plan.bm != want.bm || plan.tiles_n != want.tiles_n || plan.tiles != want.tiles)
+  const QmmPlan want = plan_qmm(M, N, K, bits, 0);
+  if (plan.bm != want.bm || plan.tiles_n != want.tiles_n || plan.tiles != want.tiles ||
+      plan.tiles_m != want.tiles_m || plan.group_m < 1 || plan.group_m > plan.tiles_m || plan.xcds < 1)
     fail("qmm: inconsistent launch plan");
   if (plan.sk_workers > 0) {
     if (plan.blocks != plan.sk_workers || int64_t(plan.sk_workers) > int64_t(plan.tiles) * (K / 64) ||

@@ -66,7 +66,32 @@ __device__ __forceinline__ u32x4 dequant8<8>(const u32x4 (&wr)[2], int i, float 
   return r;
 }
 
-// Work assignment of one launch.  Tiles are numbered M-tile major.
+// Tile order: tile t lies in group t / (group_m * tiles_n) of group_m tile
+// rows (fewer in the last group), which it walks column by column, so that
+// consecutive tiles share activation row panels (down a column) and weight
+// column panels (along a row).
+__device__ __forceinline__ void tile_rc(int tile, int tiles_m, int tiles_n, int group_m, int &tm, int &tn) {
+  const int per_group = group_m * tiles_n;
+  const int grp = tile / per_group;
+  const int first = grp * group_m;
+  const int rows = min(group_m, tiles_m - first);
+  const int within = tile - grp * per_group;
+  tm = first + within % rows;
+  tn = within / rows;
+}
+
+// The hardware deals the blocks of a launch to its L2 domains (XCDs) round
+// robin: block b runs on XCD b % xcds.  This renumbers them so that each XCD
+// takes one contiguous run of the work order (a bijection on [0, G)), and
+// the tiles that share operands share that XCD's L2.
+__device__ __forceinline__ int xcd_order(int b, int G, int xcds) {
+  if (xcds <= 1) return b;
+  const int xcd = b % xcds, idx = b / xcds;
+  const int q = G / xcds, r = G % xcds;
+  return xcd * q + min(xcd, r) + idx;
+}
+
+// Work assignment of one launch.  Tiles are numbered in tile_rc's order.
 // Data-parallel (sk_workers == 0): tiles [0, dp_tiles) are computed whole,
 // one block each; each tile after that is split into `splits` K ranges of
 // `steps_per_split` 64-wide steps, one block per range, each writing its f32
@@ -75,6 +100,9 @@ __device__ __forceinline__ u32x4 dequant8<8>(const u32x4 (&wr)[2], int i, float 
 // the tiles * K/64 iterations evenly (see the kernel); `partial` has G slots
 // and `flags` G ints, zero between launches.
 struct QmmWork {
+  int tiles_m;
+  int group_m;
+  int xcds;
   int tiles_n;
   int tiles;
   int dp_tiles;
@@ -113,8 +141,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   floatx16 acc[MB][2];
   // The product of tile `tile` over the K steps [k_begin, k_end), into acc.
   auto run = [&](const int tile, const int k_begin, const int k_end) __attribute__((always_inline)) {
-  m0 = (tile / wk.tiles_n) * BM;
-  nw = (tile % wk.tiles_n) * kTileN + wave * 64;
+  {
+    int tm, tn;
+    tile_rc(tile, wk.tiles_m, wk.tiles_n, wk.group_m, tm, tn);
+    m0 = tm * BM;
+    nw = tn * kTileN + wave * 64;
+  }
   const int k_last = k_end - 1;
 
   // Buffer windows (byte offsets fit in 32 bits: checked on the host).
@@ -380,6 +412,13 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   constexpr int kPassMB = (kWaveLds / kRowBytes) / 32 >= 4 && MB % 4 == 0 ? 4
                           : (kWaveLds / kRowBytes) / 32 >= 2 && MB % 2 == 0 ? 2 : 1;
   static_assert(kPassMB * 32 * kRowBytes <= kWaveLds, "output staging exceeds the LDS");
+  // The combine stage (gated residual or product) runs on the 16-byte
+  // pieces as they leave the LDS, on values already rounded to the output
+  // dtype (as the unfused add/multiply after the linear sees them).
+  const bool comb = ep.combine != 0;
+  auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool comb_vec = comb && a16(ep.res) && (ep.ld_res * int64_t(dtype_size_dev(ep.res_dtype))) % 16 == 0 &&
+                        (!ep.gate || a16(ep.gate));
   auto store_tile = [&](auto produce) {
     const bool vec = N % kChunkElems == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     uint8_t *wl = reinterpret_cast<uint8_t *>(xs) + wave * kWaveLds;
@@ -403,31 +442,69 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int it = 0; it < kPassMB * 32 * kCpr / 64; ++it) {
+      // Piece `it` of the slab back from the LDS to y; with the combine
+      // stage (CB) the pieces go one at a time (a loop, not unrolled: the
+      // stage's dtype cases would otherwise be copied into every piece).
+      auto readback = [&](const int it, auto cb) {
         const int idx = it * 64 + lane;
         const int row = idx / kCpr, chunk = idx % kCpr;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(wl + row * kRowBytes + chunk * 16);
+        u32x4 v = *reinterpret_cast<const u32x4 *>(wl + row * kRowBytes + chunk * 16);
         const int grow = m0 + 32 * p0 + row;
         const int gcol = nw + chunk * kChunkElems;
-        if (grow < M) {
-          OT *dst = y + int64_t(grow) * N + gcol;
-          if (vec) {
-            if (gcol < N) *reinterpret_cast<u32x4 *>(dst) = v;
-          } else {
-            // Rows not 16-byte aligned, or a ragged last chunk: element stores.
+        if (grow >= M) return;
+        OT *dst = y + int64_t(grow) * N + gcol;
+        if constexpr (decltype(cb)::value) {
+          if (gcol < N) {
+            // Whole chunk in range (vec) or the ragged last one (elementwise).
+            float f[kChunkElems];
 #pragma unroll
             for (int q = 0; q < kChunkElems; ++q) {
-              if (gcol + q < N) {
-                const uint32_t word = v[(q * int(sizeof(OT))) / 4];
-                if constexpr (sizeof(OT) == 4)
-                  dst[q] = __builtin_bit_cast(OT, word);
-                else
-                  dst[q] = OT((q & 1) ? (word >> 16) : (word & 0xffffu));
+              const uint32_t word = v[(q * int(sizeof(OT))) / 4];
+              f[q] = sizeof(OT) == 4 ? __uint_as_float(word)
+                                     : Elem<ODT>::load(OT((q & 1) ? (word >> 16) : (word & 0xffffu)));
+            }
+            if (vec && comb_vec) {
+              epi_combine_n<kChunkElems>(ep, grow, gcol, true, f);
+            } else {
+#pragma unroll
+              for (int q = 0; q < kChunkElems; ++q)
+                if (gcol + q < N) f[q] = epi_combine(ep, f[q], grow, gcol + q);
+            }
+#pragma unroll
+            for (int q = 0; q < kChunkElems; ++q) {
+              const uint32_t bits = sizeof(OT) == 4 ? __float_as_uint(f[q]) : uint32_t(Elem<ODT>::store(f[q]));
+              if constexpr (sizeof(OT) == 4) {
+                v[q] = bits;
+              } else {
+                const int wi = q >> 1;
+                v[wi] = (q & 1) ? ((v[wi] & 0xffffu) | (bits << 16)) : ((v[wi] & 0xffff0000u) | bits);
               }
             }
           }
         }
+        if (vec) {
+          if (gcol < N) *reinterpret_cast<u32x4 *>(dst) = v;
+        } else {
+          // Rows not 16-byte aligned, or a ragged last chunk: element stores.
+#pragma unroll
+          for (int q = 0; q < kChunkElems; ++q) {
+            if (gcol + q < N) {
+              const uint32_t word = v[(q * int(sizeof(OT))) / 4];
+              if constexpr (sizeof(OT) == 4)
+                dst[q] = __builtin_bit_cast(OT, word);
+              else
+                dst[q] = OT((q & 1) ? (word >> 16) : (word & 0xffffu));
+            }
+          }
+        }
+      };
+      constexpr int kPieces = kPassMB * 32 * kCpr / 64;
+      if (comb) {
+#pragma unroll 1
+        for (int it = 0; it < kPieces; ++it) readback(it, std::integral_constant<bool, true>{});
+      } else {
+#pragma unroll
+        for (int it = 0; it < kPieces; ++it) readback(it, std::integral_constant<bool, false>{});
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -528,8 +605,13 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   // bounded all the same (a flag that never comes leaves the tile without
   // that partial rather than hanging).  The three kinds are three inlined
   // copies of the K loop: a loop over mixed pieces keeps too much alive.
-  const int g = blockIdx.x;
   if constexpr (!SKM) {
+    // Whole tiles and split ranges are renumbered separately: the whole
+    // tiles come first in dispatch order (the first round of the launch)
+    // and must stay there, ahead of the split ranges.
+    const int b = int(blockIdx.x);
+    const int g = b < wk.dp_tiles ? xcd_order(b, wk.dp_tiles, wk.xcds)
+                                  : wk.dp_tiles + xcd_order(b - wk.dp_tiles, int(gridDim.x) - wk.dp_tiles, wk.xcds);
     // Data-parallel launch: block b computes tile b whole, or (b past
     // dp_tiles) one K range of a split tile, whose partial the reduction
     // kernel that follows on the stream adds.  (An instantiation of its own:
@@ -553,6 +635,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     finish_tile();
     return;
   }
+  // Stream-K keeps the dispatch order: its waits point to lower block
+  // indices, which must be dispatched first.
+  const int g = blockIdx.x;
   const bool sk = true;
   int tail_tile = -1, tail_kb = 0, tail_ke = 0; // a partial piece, stored in slot g
   int64_t tail_slot = 0;
@@ -633,8 +718,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
 template <int ODT>
 __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
                                                          const float *__restrict__ partial,
-                                                         int M, int N, int bm, int tiles_n,
-                                                         int dp_tiles, int splits,
+                                                         int M, int N, int bm, int tiles_m, int tiles_n,
+                                                         int group_m, int dp_tiles, int splits,
                                                          kern::Epilogue ep) {
   const int per_tile = bm * (kTileN / 4); // float4 pieces of one partial tile
   const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -647,8 +732,10 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
   const int row = 32 * mb + 8 * q + 4 * (lane >> 5);  // first of four rows
   const int col = wave * 64 + 32 * j + (lane & 31);
   const int tile = dp_tiles + sk;
-  const int grow = (tile / tiles_n) * bm + row;
-  const int gcol = (tile % tiles_n) * kTileN + col;
+  int tm, tn;
+  tile_rc(tile, tiles_m, tiles_n, group_m, tm, tn);
+  const int grow = tm * bm + row;
+  const int gcol = tn * kTileN + col;
   if (grow >= M || gcol >= N) return;
   const float4 *src = reinterpret_cast<const float4 *>(partial) + int64_t(sk) * splits * per_tile + within;
   float4 sum = src[0];
@@ -670,7 +757,13 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
   const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
   for (int u = 0; u < 4; ++u)
-    if (grow + u < M) y[int64_t(grow + u) * N + gcol] = Elem<ODT>::store(epi_apply(ep, s4[u], b));
+    if (grow + u < M) {
+      float v = Elem<ODT>::round(epi_apply(ep, s4[u], b));
+      // The combine stage on the value rounded to the output dtype, as in the
+      // tile kernel's store.
+      if (ep.combine) v = epi_combine(ep, v, grow + u, gcol);
+      y[int64_t(grow + u) * N + gcol] = Elem<ODT>::store(v);
+    }
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int BM>
@@ -678,7 +771,7 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
                   const void *s, const void *b, int M, int N, int K, int gs,
                   const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
                   const kern::Epilogue &ep, hipStream_t st) {
-  const QmmWork wk{plan.tiles_n, plan.tiles, plan.dp_tiles, plan.splits, plan.steps_per_split, plan.sk_workers,
+  const QmmWork wk{plan.tiles_m, plan.group_m, plan.xcds, plan.tiles_n, plan.tiles, plan.dp_tiles, plan.splits, plan.steps_per_split, plan.sk_workers,
                    ws.partial, ws.flags};
   const dim3 grid(plan.blocks);
   auto *yp = static_cast<typename Elem<ODT>::T *>(y);
@@ -715,7 +808,7 @@ void launch_qmm_t(void *y, const void *x, int64_t ldx, const uint32_t *w,
     hip_check(hipGetLastError(), "qmm launch");
     const int64_t threads = int64_t(sk_tiles) * BM * (kTileN / 4);
     qmm_reduce_kernel<ODT><<<dim3(unsigned(threads / 256)), 256, 0, st>>>(
-        yp, ws.partial, M, N, BM, plan.tiles_n, plan.dp_tiles, plan.splits, ep);
+        yp, ws.partial, M, N, BM, plan.tiles_m, plan.tiles_n, plan.group_m, plan.dp_tiles, plan.splits, ep);
   }
 }
 

@@ -77,7 +77,7 @@ extern "C" int sdq_quantized_matmul_noalloc(void *y, int y_dtype, const void *x,
       return 0;
     }
     // The fixed scratch takes the data-parallel plan only (no stream-K flags).
-    const kern::QmmPlan plan = kern::plan_qmm(M, N, K, cu_count(device), kScratchFloats, false);
+    const kern::QmmPlan plan = kern::plan_qmm(M, N, K, bits, cu_count(device), kScratchFloats, false);
     if (plan.partial_floats > kScratchFloats)
       fail("the launch needs " + std::to_string(plan.partial_floats * sizeof(float)) +
            " bytes of split-K scratch; the no-allocation entry point holds " +

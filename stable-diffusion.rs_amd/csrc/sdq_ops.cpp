@@ -68,22 +68,17 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
     kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
               plan, ep, stream);
   } else {
-    kern::QmmPlan plan = kern::plan_qmm(M, N, K, cu_count(device));
+    kern::QmmPlan plan = kern::plan_qmm(M, N, K, bits, cu_count(device));
     kern::SplitWorkspace ws;
     if (plan.dp_tiles < plan.tiles || plan.sk_workers > 0) {
       float *base = stream_workspace(device, stream, plan.partial_floats);
       ws.flags = reinterpret_cast<int *>(base);
       ws.partial = base + kWorkspaceHeaderFloats;
     }
-    // The tile kernel fuses bias and activation; the combine stage follows
-    // as one in-place pass (the tile store with it grows the kernel ~6x).
-    kern::Epilogue ep_mm = ep;
-    ep_mm.combine = 0;
-    ep_mm.res = nullptr;
-    ep_mm.gate = nullptr;
+    // The whole epilogue (bias, activation, combine stage) runs in the tile
+    // kernel's store, or in the reduction of split tiles.
     kern::qmm(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ws, ep_mm, stream);
-    kern::combine_inplace(y, y_dtype, M, N, ep, stream);
+              plan, ws, ep, stream);
   }
 }
 

@@ -172,7 +172,7 @@ def _host_array(sdq, vals, dt):
 @pytest.mark.parametrize("gdt", [None, "bf16", "f16", "f32"])
 @pytest.mark.parametrize("mode", ["gated", "product"])
 def test_combine_over_operand_dtypes(oracle, sdq, stream, M, N, sdt, rdt, gdt, mode):
-    # The combine stage after the large-M kernel (M > 32), for every output,
+    # The combine stage in the large-M kernel's store (M > 32), for every output,
     # residual and gate dtype: against the f64 composition, and bit for bit
     # against the unfused sequence where that sequence rounds the same way
     # (a product, or a residual without gate: one rounding in both).

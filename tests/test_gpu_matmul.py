@@ -294,8 +294,8 @@ def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
 @pytest.mark.parametrize("M,N,K,bits", [
     (1, 200, 512, 4),       # small-M kernel: combine in the store
     (16, 64, 8192, 8),      # small-M kernel, split K
-    (100, 300, 256, 4),     # tile kernel, then the in-place combine pass
-    (300, 512, 8192, 4),    # tile kernel with split K and the reduction kernel
+    (100, 300, 256, 4),     # tile kernel: combine in its store
+    (300, 512, 8192, 4),    # tile kernel with split K: combine in the reduction kernel
 ])
 @pytest.mark.parametrize("mode", ["gated", "residual", "product"])
 def test_linear_combine_matches_the_composition(oracle, sdq, stream, M, N, K, bits, mode):
