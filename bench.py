@@ -100,7 +100,7 @@ def roofline_point(M, N, K, bits, ms):
             "frac": round(frac, 4)}
 
 
-TRAFFIC_FILE = REPO / "profiles" / "bench_config2_hbm_traffic.md"
+TRAFFIC_FILE = REPO / "profiles" / "qmm_config2_step.md"
 
 
 def measured_traffic(label):
