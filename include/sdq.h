@@ -374,6 +374,23 @@ int sdq_flux_attention(sdq_array *res, sdq_array qkv_a, sdq_array q_norm_a,
                        sdq_array k_norm_b, sdq_array pe_cos, sdq_array pe_sin,
                        int heads, float scale, float eps, sdq_stream s);
 
+/* The single block's linear1 through to linear2's input (flux.rs:440-465):
+ * projected = linear1(x) (the quantized linear w/scales/biases plus bias);
+ * its first 3*heads*128 columns go to the attention above (q/k norm, rope,
+ * sdpa, merge_heads) and its remaining (MLP) columns through gelu_approx;
+ * the result is concat([attention, gelu(mlp)], axis 2), [B, T, heads*128 +
+ * mlp].  One matmul launch writes both parts (the MLP part straight into the
+ * result, GELU applied in its epilogue to the f32 value, so it can differ
+ * from the unfused sequence by one rounding), then the attention writes the
+ * result's first columns.  x [B, T, hidden]; 3*heads*128 must be a multiple
+ * of 256 (an even head count).  No mlx-c counterpart. */
+int sdq_flux_single_linear1_attention(sdq_array *res, sdq_array x, sdq_array w,
+                                      sdq_array scales, sdq_array biases, sdq_array bias,
+                                      sdq_optional_int group_size, sdq_optional_int bits,
+                                      const char *mode, sdq_array q_norm, sdq_array k_norm,
+                                      sdq_array pe_cos, sdq_array pe_sin, int heads,
+                                      float scale, float eps, sdq_stream s);
+
 /* ---- raw-pointer entry point ------------------------------------------------- */
 
 /* The kernel behind sdq_quantized_matmul on caller-owned device memory:
@@ -419,6 +436,22 @@ int sdq_quantized_matmul_noalloc(void *y, int y_dtype, const void *x, int x_dtyp
                                  int64_t N, int64_t K, int group_size, int bits,
                                  const void *bias, int bias_dtype, int activation,
                                  void *hip_stream);
+
+/* sdq_quantized_matmul_epilogue_raw writing its output to two places:
+ * columns [0, split) to y (row stride ldy elements, activation), columns
+ * [split, N) to y2 (row stride ldy2, column n at y2 + (n - split),
+ * activation2).  split is a multiple of 256 inside (0, N).  It replaces the
+ * narrow / gelu_approx / concat calls after Flux's single-block linear1
+ * (flux.rs:440-469: q, k, v columns to the attention, GELU'd MLP columns
+ * into linear2's input after the attention output).  No mlx-c counterpart:
+ * the reference issues those calls separately. */
+int sdq_quantized_linear_split_raw(void *y, int64_t ldy, int activation, void *y2,
+                                   int64_t ldy2, int activation2, int64_t split,
+                                   int y_dtype, const void *x, int x_dtype, int64_t ldx,
+                                   const uint32_t *w, const void *scales,
+                                   const void *biases, int s_dtype, int64_t M,
+                                   int64_t N, int64_t K, int group_size, int bits,
+                                   const void *bias, int bias_dtype, void *hip_stream);
 
 /* tanh-GELU on caller-owned device memory (dtype float32/bfloat16/float16),
  * enqueued on `hip_stream`: the elementwise step between the two Flux MLP

@@ -227,6 +227,22 @@ __device__ __forceinline__ float epi_apply(const kern::Epilogue &ep, float v, fl
   return ep.act == 1 ? gelu_approx_f(v) : v;
 }
 
+// The output layout of the epilogue: where column n of row m goes, and the
+// activation of that column (kern::Epilogue: y with row stride ldy, or y2
+// for columns past the split).
+template <typename OT>
+__device__ __forceinline__ OT *epi_dst(const kern::Epilogue &ep, OT *y, int64_t N, int64_t m, int64_t n) {
+  if (ep.split > 0 && n >= ep.split) return static_cast<OT *>(ep.y2) + m * ep.ldy2 + (n - ep.split);
+  return y + m * (ep.ldy > 0 ? ep.ldy : N) + n;
+}
+__device__ __forceinline__ int epi_act(const kern::Epilogue &ep, int64_t n) {
+  return ep.split > 0 && n >= ep.split ? ep.act2 : ep.act;
+}
+__device__ __forceinline__ float epi_apply_col(const kern::Epilogue &ep, float v, float bias, int64_t n) {
+  v += bias;
+  return epi_act(ep, n) == 1 ? gelu_approx_f(v) : v;
+}
+
 // The combine stage of the epilogue for output element (m, n).
 __device__ __forceinline__ float epi_combine(const kern::Epilogue &ep, float v, int64_t m, int64_t n) {
   if (ep.combine == 0) return v;

@@ -51,6 +51,13 @@ void gguf_quantize(const uint8_t *raw, int type, int64_t rows, int64_t cols, int
 // combine stage to the f32 value in its store; the large-M kernel applies it
 // in its store (or its reduction kernel) to v rounded to the output dtype, as
 // the unfused sequence does.
+//
+// Output layout: y has row stride ldy (0: N).  With split > 0 (a multiple of
+// 256, below N) columns [split, N) go instead to y2, row stride ldy2, column
+// n at y2 + (n - split), with activation act2 (Flux's single block: linear1's
+// q/k/v columns to one buffer, its GELU'd MLP columns into linear2's input
+// after the attention output, flux.rs:440-469).  No combine stage with a
+// split.
 struct Epilogue {
   const void *bias = nullptr;
   int bias_dtype = 0;
@@ -61,6 +68,11 @@ struct Epilogue {
   const void *gate = nullptr;
   int gate_dtype = 0;
   int combine = 0;
+  int64_t ldy = 0;
+  int64_t split = 0;
+  void *y2 = nullptr;
+  int64_t ldy2 = 0;
+  int act2 = 0;
 };
 
 inline bool epi_dtype_ok(int dt) {
@@ -70,6 +82,12 @@ inline bool epi_dtype_ok(int dt) {
 inline bool epilogue_ok(const Epilogue &ep) {
   if (ep.bias && !epi_dtype_ok(ep.bias_dtype)) return false;
   if (ep.act != 0 && ep.act != 1) return false;
+  if (ep.ldy < 0) return false;
+  if (ep.split != 0) {
+    if (ep.split < 0 || ep.split % 256 != 0 || !ep.y2 || ep.ldy2 < 1) return false;
+    if (ep.act2 != 0 && ep.act2 != 1) return false;
+    if (ep.combine != 0) return false;
+  }
   if (ep.combine == 0) return true;
   if (ep.combine != 1 && ep.combine != 2) return false;
   if (!ep.res || !epi_dtype_ok(ep.res_dtype)) return false;

@@ -420,7 +420,13 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   const bool comb_vec = comb && a16(ep.res) && (ep.ld_res * int64_t(dtype_size_dev(ep.res_dtype))) % 16 == 0 &&
                         (!ep.gate || a16(ep.gate));
   auto store_tile = [&](auto produce) {
-    const bool vec = N % kChunkElems == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    // Output layout (kern::Epilogue): a tile lies wholly on one side of the
+    // split (a multiple of 256).
+    const bool hi = ep.split > 0 && nw - wave * 64 >= ep.split;
+    OT *const ybase = hi ? static_cast<OT *>(ep.y2) : y;
+    const int64_t ldo = hi ? ep.ldy2 : (ep.ldy > 0 ? ep.ldy : int64_t(N));
+    const int col0 = hi ? int(ep.split) : 0;
+    const bool vec = N % kChunkElems == 0 && a16(ybase) && (ldo * int64_t(sizeof(OT))) % 16 == 0;
     uint8_t *wl = reinterpret_cast<uint8_t *>(xs) + wave * kWaveLds;
 #pragma unroll
     for (int p0 = 0; p0 < MB; p0 += kPassMB) {
@@ -452,7 +458,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
         const int grow = m0 + 32 * p0 + row;
         const int gcol = nw + chunk * kChunkElems;
         if (grow >= M) return;
-        OT *dst = y + int64_t(grow) * N + gcol;
+        OT *dst = ybase + int64_t(grow) * ldo + (gcol - col0);
         if constexpr (decltype(cb)::value) {
           if (gcol < N) {
             // Whole chunk in range (vec) or the ragged last one (elementwise).
@@ -580,7 +586,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
         }
       });
     };
-    if (ep.act == 1)
+    const bool hi = ep.split > 0 && nw - wave * 64 >= ep.split;
+    if ((hi ? ep.act2 : ep.act) == 1)
       finish(std::integral_constant<bool, true>{});
     else
       finish(std::integral_constant<bool, false>{});
@@ -758,11 +765,11 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
 #pragma unroll
   for (int u = 0; u < 4; ++u)
     if (grow + u < M) {
-      float v = Elem<ODT>::round(epi_apply(ep, s4[u], b));
+      float v = Elem<ODT>::round(epi_apply_col(ep, s4[u], b, gcol));
       // The combine stage on the value rounded to the output dtype, as in the
       // tile kernel's store.
       if (ep.combine) v = epi_combine(ep, v, grow + u, gcol);
-      y[int64_t(grow + u) * N + gcol] = Elem<ODT>::store(v);
+      *epi_dst(ep, y, N, grow + u, gcol) = Elem<ODT>::store(v);
     }
 }
 

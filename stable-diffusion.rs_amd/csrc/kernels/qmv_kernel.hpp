@@ -541,7 +541,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     for (int e = 0; e < 4; ++e) {
       const int m = mb * 16 + 4 * lh + e;
       if (m < M)
-        y[int64_t(m) * N + n] = Elem<ODT>::store(epi_combine(ep, epi_apply(ep, acc[mb][e], bn), m, n));
+        *epi_dst(ep, y, N, m, n) = Elem<ODT>::store(epi_combine(ep, epi_apply_col(ep, acc[mb][e], bn, n), m, n));
     }
 }
 

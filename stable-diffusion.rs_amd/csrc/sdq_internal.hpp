@@ -136,6 +136,29 @@ void same_device(const ArrayImpl *a, const StreamImpl *s, const char *name);
 // Reports `msg` for op `op` through the installed handler.
 void report(const char *op, const char *msg);
 
+namespace kern {
+struct Epilogue;
+}
+
+// y = x @ dequantize(w).T on device pointers with the epilogue `ep` (its
+// output layout included), on `stream`; picks the kernel by M
+// (sdq_ops.cpp).
+void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
+                     const uint32_t *w, const void *scales, const void *biases,
+                     int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
+                     int device, hipStream_t stream, const kern::Epilogue &ep);
+
+// The Flux attention (sdq_ops_block.cpp): output shape of the qkv inputs,
+// and the op writing its merged-heads output at `out` with row stride
+// `ld_out` elements.
+struct FluxAttnShape {
+  int B = 0, N = 0, dtype = SDQ_FLOAT32;
+};
+FluxAttnShape flux_attention_shape(sdq_array qkv_a, sdq_array qkv_b, int heads, const StreamImpl *st);
+void flux_attention_into(void *out, int64_t ld_out, sdq_array qkv_a, sdq_array q_norm_a, sdq_array k_norm_a,
+                         sdq_array qkv_b, sdq_array q_norm_b, sdq_array k_norm_b, sdq_array pe_cos,
+                         sdq_array pe_sin, int heads, float scale, float eps, const StreamImpl *st);
+
 } // namespace sdq
 
 // Wraps a C entry point body: exceptions become status 1 plus a message.

@@ -53,12 +53,24 @@ void check_group_bits(int gs, int bits) {
          " is not supported. The supported bits are 2, 4 and 8.");
 }
 
-// y = x @ dequantize(w).T on device pointers; picks the kernel by M.
+} // namespace
+
 void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
                      const uint32_t *w, const void *scales, const void *biases,
                      int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
-                     int device, hipStream_t stream, const kern::Epilogue &ep = {}) {
+                     int device, hipStream_t stream, const kern::Epilogue &ep) {
   if (M == 0 || N == 0) return;
+  if (ep.split != 0) {
+    if (ep.split % 256 != 0 || ep.split <= 0 || ep.split >= N)
+      fail("the output split must be a multiple of 256 inside (0, N), got " + std::to_string(ep.split) +
+           " for N = " + std::to_string(N));
+    if (!ep.y2) fail("the output split needs its second destination");
+    if (ep.ldy != 0 && ep.ldy < ep.split) fail("the first destination's row stride is shorter than the split");
+    if (ep.ldy2 < N - ep.split) fail("the second destination's row stride is shorter than N - split");
+    if (ep.combine != 0) fail("the output split takes no combine stage");
+  } else if (ep.ldy != 0 && ep.ldy < N) {
+    fail("the output row stride is shorter than N");
+  }
   if (gs != 64 && gs != 128)
     fail("the quantized matmul kernels take group size 64 or 128, got " + std::to_string(gs));
   if (bits != 4 && bits != 8)
@@ -81,6 +93,8 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
               plan, ws, ep, stream);
   }
 }
+
+namespace {
 
 } // namespace
 
@@ -202,19 +216,21 @@ namespace {
 
 // quantized_matmul with an optional output epilogue (bias [N], activation),
 // shared by sdq_quantized_matmul and sdq_quantized_linear.
-void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
-                           sdq_array biases, bool transpose, sdq_optional_int group_size,
-                           sdq_optional_int bits, const char *mode, sdq_stream s,
-                           sdq_array bias, int activation, sdq_array residual = sdq_array{nullptr},
-                           sdq_array gate = sdq_array{nullptr}, int combine = SDQ_COMBINE_NONE) {
-    StreamImpl *st = stream_of(s, "quantized_matmul");
+// The quantized weight and activation operands of a linear, checked as
+// mlx_quantized_matmul checks them (transpose = true).
+struct QOperands {
+  ArrayImpl *xa, *wa, *sa, *ba;
+  int64_t N, K;
+  int gs, nb;
+};
+
+QOperands quantized_operands(sdq_array x, sdq_array w, sdq_array scales, sdq_array biases,
+                             sdq_optional_int group_size, sdq_optional_int bits, const char *mode,
+                             const StreamImpl *st) {
     check_mode(mode, sdq_array{nullptr});
     const int gs = opt_or(group_size, 64);
     const int nb = opt_or(bits, 4);
     check_group_bits(gs, nb);
-    if (!transpose)
-      fail("transpose=false (x @ W with W quantized along its output axis) is not "
-           "implemented; the diffusers [out, in] layout uses transpose=true");
     ArrayImpl *xa = array_of(x, "quantized_matmul", "x");
     ArrayImpl *wa = array_of(w, "quantized_matmul", "w");
     ArrayImpl *sa = array_of(scales, "quantized_matmul", "scales");
@@ -244,17 +260,37 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
       fail("Last dimension of first input with shape " + shape_str(xa->shape) +
            " must match the dequantized weight's input width " + std::to_string(K) +
            " (weight " + shape_str(wa->shape) + ", bits=" + std::to_string(nb) + ")");
+    return QOperands{xa, wa, sa, ba, N, K, gs, nb};
+}
+
+// The bias of a linear: a float array of N values, or none.
+ArrayImpl *linear_bias(sdq_array bias, int64_t N, const StreamImpl *st, kern::Epilogue &ep) {
+    if (!bias.ctx) return nullptr;
+    ArrayImpl *bb = array_of(bias, "quantized_linear", "bias");
+    same_device(bb, st, "bias");
+    if (!is_float_dtype(bb->dtype) || bb->size != size_t(N) || (!bb->shape.empty() && bb->shape.back() != N))
+      fail("bias must be a float array of shape [" + std::to_string(N) + "], got " +
+           shape_str(bb->shape) + " " + dtype_name(bb->dtype));
+    ep.bias = bb->data();
+    ep.bias_dtype = bb->dtype;
+    return bb;
+}
+
+void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                           sdq_array biases, bool transpose, sdq_optional_int group_size,
+                           sdq_optional_int bits, const char *mode, sdq_stream s,
+                           sdq_array bias, int activation, sdq_array residual = sdq_array{nullptr},
+                           sdq_array gate = sdq_array{nullptr}, int combine = SDQ_COMBINE_NONE) {
+    StreamImpl *st = stream_of(s, "quantized_matmul");
+    if (!transpose)
+      fail("transpose=false (x @ W with W quantized along its output axis) is not "
+           "implemented; the diffusers [out, in] layout uses transpose=true");
+    const QOperands q = quantized_operands(x, w, scales, biases, group_size, bits, mode, st);
+    ArrayImpl *xa = q.xa, *wa = q.wa, *sa = q.sa, *ba = q.ba;
+    const int64_t N = q.N, K = q.K;
+    const int gs = q.gs, nb = q.nb;
     kern::Epilogue ep;
-    ArrayImpl *bb = nullptr;
-    if (bias.ctx) {
-      bb = array_of(bias, "quantized_linear", "bias");
-      same_device(bb, st, "bias");
-      if (!is_float_dtype(bb->dtype) || bb->size != size_t(N) || (!bb->shape.empty() && bb->shape.back() != N))
-        fail("bias must be a float array of shape [" + std::to_string(N) + "], got " +
-             shape_str(bb->shape) + " " + dtype_name(bb->dtype));
-      ep.bias = bb->data();
-      ep.bias_dtype = bb->dtype;
-    }
+    ArrayImpl *bb = linear_bias(bias, N, st, ep);
     if (activation != SDQ_ACT_NONE && activation != SDQ_ACT_GELU_APPROX)
       fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(activation));
     ep.act = activation;
@@ -356,7 +392,7 @@ int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, i
     int device = 0;
     hip_check(hipGetDevice(&device), "hipGetDevice");
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
-                    group_size, bits, device, static_cast<hipStream_t>(hip_stream));
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), kern::Epilogue{});
   });
 }
 
@@ -385,6 +421,85 @@ int sdq_quantized_matmul_epilogue_raw(void *y, int y_dtype, const void *x, int x
     if (!kern::epilogue_ok(ep)) fail("bad epilogue");
     matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
                     group_size, bits, device, static_cast<hipStream_t>(hip_stream), ep);
+  });
+}
+
+int sdq_quantized_linear_split_raw(void *y, int64_t ldy, int activation, void *y2, int64_t ldy2,
+                                   int activation2, int64_t split, int y_dtype, const void *x, int x_dtype,
+                                   int64_t ldx, const uint32_t *w, const void *scales, const void *biases,
+                                   int s_dtype, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                   const void *bias, int bias_dtype, void *hip_stream) {
+  SDQ_GUARD("quantized_linear_split_raw", {
+    if (M < 0 || N < 0 || K <= 0) fail("M, N must be >= 0 and K > 0");
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(s_dtype) || !is_float_dtype(y_dtype))
+      fail("dtypes must be float32, bfloat16 or float16");
+    if (bias && !is_float_dtype(bias_dtype))
+      fail("bias dtype must be float32, bfloat16 or float16");
+    for (int a : {activation, activation2})
+      if (a != SDQ_ACT_NONE && a != SDQ_ACT_GELU_APPROX)
+        fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(a));
+    check_group_bits(group_size, bits);
+    if (K % group_size != 0) fail("K must be a multiple of group_size");
+    if (M > 0 && N > 0 && (!y || !y2 || !x || !w || !scales || !biases)) fail("NULL pointer argument");
+    if (split <= 0) fail("split must be positive (sdq_quantized_matmul_epilogue_raw has no split)");
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    kern::Epilogue ep;
+    ep.bias = bias;
+    ep.bias_dtype = bias ? bias_dtype : 0;
+    ep.act = activation;
+    ep.ldy = ldy;
+    ep.split = split;
+    ep.y2 = y2;
+    ep.ldy2 = ldy2;
+    ep.act2 = activation2;
+    if (!kern::epilogue_ok(ep)) fail("bad epilogue: split must be a multiple of 256, row strides positive");
+    matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), ep);
+  });
+}
+
+int sdq_flux_single_linear1_attention(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                                      sdq_array biases, sdq_array bias, sdq_optional_int group_size,
+                                      sdq_optional_int bits, const char *mode, sdq_array q_norm,
+                                      sdq_array k_norm, sdq_array pe_cos, sdq_array pe_sin, int heads,
+                                      float scale, float eps, sdq_stream s) {
+  SDQ_GUARD("flux_single_linear1_attention", {
+    StreamImpl *st = stream_of(s, "flux_single_linear1_attention");
+    if (!res) fail("result pointer is NULL");
+    const QOperands q = quantized_operands(x, w, scales, biases, group_size, bits, mode, st);
+    if (q.xa->shape.size() != 3) fail("x must be [batch, tokens, hidden], got " + shape_str(q.xa->shape));
+    if (heads <= 0) fail("heads must be positive");
+    const int64_t h = int64_t(heads) * 128;
+    const int64_t qkv_w = 3 * h, mlp = q.N - qkv_w;
+    if (mlp <= 0) fail("linear1 must have more than 3 * heads * 128 outputs (q, k, v, then the MLP)");
+    if (qkv_w % 256 != 0) fail("3 * heads * 128 must be a multiple of 256 (an even head count)");
+    kern::Epilogue ep;
+    ArrayImpl *bb = linear_bias(bias, q.N, st, ep);
+    const int out_dtype = promote_float(q.xa->dtype, q.sa->dtype);
+    const int B = q.xa->shape[0], T = q.xa->shape[1];
+    if (bb) order_after(bb, st);
+    order_after(q.xa, st);
+    order_after(q.wa, st);
+    order_after(q.sa, st);
+    order_after(q.ba, st);
+    // linear1's q/k/v columns go to a buffer of their own; its MLP columns,
+    // through GELU, to linear2's input after the attention's columns.
+    auto qkv = make_array({B, T, int(qkv_w)}, out_dtype, *st);
+    auto joined = make_array({B, T, int(h + mlp)}, out_dtype, *st);
+    ep.act = SDQ_ACT_NONE;
+    ep.ldy = qkv_w;
+    ep.split = qkv_w;
+    ep.y2 = static_cast<unsigned char *>(joined->data()) + size_t(h) * dtype_size(out_dtype);
+    ep.ldy2 = h + mlp;
+    ep.act2 = SDQ_ACT_GELU_APPROX;
+    const int64_t M = int64_t(B) * T;
+    matmul_dispatch(qkv->data(), out_dtype, q.xa->data(), q.xa->dtype, q.K,
+                    static_cast<const uint32_t *>(q.wa->data()), q.sa->data(), q.ba->data(), q.sa->dtype,
+                    M, q.N, q.K, q.gs, q.nb, st->device, st->stream, ep);
+    flux_attention_into(joined->data(), h + mlp, sdq_array{qkv.get()}, q_norm, k_norm, sdq_array{nullptr},
+                        sdq_array{nullptr}, sdq_array{nullptr}, pe_cos, pe_sin, heads, scale, eps, st);
+    set_result(res, std::move(joined));
   });
 }
 

@@ -212,82 +212,124 @@ int sdq_fast_scaled_dot_product_attention(sdq_array *res, sdq_array queries, sdq
   });
 }
 
+} // extern "C"
+
+namespace sdq {
+
+// The Flux attention from q/k/v projections to the merged-heads output,
+// written at `out` with row stride `ld_out` elements (a token's heads * 128
+// values are contiguous): sdq_flux_attention allocates [B, N, heads * 128];
+// the fused single-block op writes the first heads * 128 columns of
+// linear2's input.  Returns the output dtype (qkv_a's).
+FluxAttnShape flux_attention_shape(sdq_array qkv_a, sdq_array qkv_b, int heads, const StreamImpl *st) {
+  const char *op = "flux_attention";
+  constexpr int D = 128;
+  if (heads <= 0) fail("heads must be positive");
+  const int64_t width = int64_t(3) * heads * D;
+  FluxAttnShape r;
+  sdq_array qkv[2] = {qkv_a, qkv_b};
+  for (int i = 0; i < 2; ++i) {
+    if (i == 1 && !qkv[1].ctx) break;
+    const ArrayImpl *x = float_input(qkv[i], op, i ? "qkv_b" : "qkv_a", st);
+    const auto &sh = x->shape;
+    if (sh.size() != 3 || sh[2] < width)
+      fail("mlx: qkv got " + shape_str(sh) + "; need [batch, tokens, >= 3 * heads * 128]");
+    if (i == 0) {
+      r.B = sh[0];
+      r.dtype = x->dtype;
+    } else {
+      if (sh[0] != r.B) fail("the two streams must have one batch size");
+      if (x->dtype != r.dtype) fail("the two streams must have one dtype");
+    }
+    r.N += sh[1];
+  }
+  return r;
+}
+
+void flux_attention_into(void *out, int64_t ld_out, sdq_array qkv_a, sdq_array q_norm_a, sdq_array k_norm_a,
+                         sdq_array qkv_b, sdq_array q_norm_b, sdq_array k_norm_b, sdq_array pe_cos,
+                         sdq_array pe_sin, int heads, float scale, float eps, const StreamImpl *st) {
+  const char *op = "flux_attention";
+  constexpr int D = 128;
+  if (heads <= 0) fail("heads must be positive");
+  if (ld_out < int64_t(heads) * D) fail("the output row stride is shorter than heads * 128");
+  struct Src {
+    ArrayImpl *x = nullptr;
+    const ArrayImpl *qn = nullptr, *kn = nullptr;
+    int n = 0;
+  } src[2];
+  sdq_array qkv[2] = {qkv_a, qkv_b}, qn[2] = {q_norm_a, q_norm_b}, kn[2] = {k_norm_a, k_norm_b};
+  const FluxAttnShape shp = flux_attention_shape(qkv_a, qkv_b, heads, st);
+  for (int i = 0; i < 2; ++i) {
+    if (i == 1 && !qkv[1].ctx) break;
+    src[i].x = float_input(qkv[i], op, i ? "qkv_b" : "qkv_a", st);
+    src[i].n = src[i].x->shape[1];
+    if (!qn[i].ctx || !kn[i].ctx) fail("the q and k norm scales are required");
+    src[i].qn = norm_param(qn[i], op, "query_norm.scale", D, st);
+    src[i].kn = norm_param(kn[i], op, "key_norm.scale", D, st);
+  }
+  const int B = shp.B;
+  const int wdt = src[0].qn->dtype;
+  for (int i = 0; i < 2; ++i)
+    if (src[i].x && (src[i].qn->dtype != wdt || src[i].kn->dtype != wdt))
+      fail("the norm scales must have one dtype");
+  const int N = shp.N;
+  ArrayImpl *ca = float_input(pe_cos, op, "pe.cos", st);
+  ArrayImpl *sa = float_input(pe_sin, op, "pe.sin", st);
+  for (const ArrayImpl *p : {ca, sa}) {
+    if (p->dtype != SDQ_FLOAT32) fail("the rotary tables must be float32");
+    if (int64_t(p->size) != int64_t(N) * (D / 2))
+      fail("the rotary tables must hold [1, " + std::to_string(N) + ", 64] values, got " + shape_str(p->shape));
+  }
+  const int64_t ldt = kern::attention_vt_stride(N);
+  auto q = make_array({B, heads, N, D}, SDQ_BFLOAT16, *st);
+  auto k = make_array({B, heads, N, D}, SDQ_BFLOAT16, *st);
+  auto vt = make_array({B, heads, D, int(ldt)}, SDQ_BFLOAT16, *st);
+  kern::FluxPrepSrc pa, pb;
+  for (int i = 0; i < 2; ++i) {
+    if (!src[i].x) continue;
+    kern::FluxPrepSrc &p = i ? pb : pa;
+    p.qkv = src[i].x->data();
+    p.ld = src[i].x->shape[2];
+    p.sb = int64_t(src[i].n) * src[i].x->shape[2];
+    p.qn = src[i].qn->data();
+    p.kn = src[i].kn->data();
+  }
+  kern::flux_attention_prep(pa, pb, src[0].x->dtype, wdt, src[0].n, src[1].n, B, heads, eps,
+                            static_cast<const float *>(ca->data()), static_cast<const float *>(sa->data()),
+                            static_cast<uint16_t *>(q->data()), static_cast<uint16_t *>(k->data()),
+                            static_cast<uint16_t *>(vt->data()), ldt, st->stream);
+  // merge_heads' layout: token rows of heads * 128 values, row stride ld_out.
+  kern::AttnArgs a;
+  a.q = static_cast<const uint16_t *>(q->data());
+  a.k = static_cast<const uint16_t *>(k->data());
+  a.vt = static_cast<const uint16_t *>(vt->data());
+  a.o = out;
+  a.q_sn = D, a.q_sh = int64_t(N) * D, a.q_sb = int64_t(heads) * N * D;
+  a.k_sn = D, a.k_sh = a.q_sh, a.k_sb = a.q_sb;
+  a.v_sd = ldt, a.v_sh = int64_t(D) * ldt, a.v_sb = int64_t(heads) * D * ldt;
+  a.o_sn = ld_out, a.o_sh = D, a.o_sb = int64_t(N) * ld_out;
+  a.B = B, a.H = heads, a.group = 1, a.Nq = N, a.Nk = N, a.D = D;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  kern::attention(a, shp.dtype, st->stream);
+}
+
+} // namespace sdq
+
+extern "C" {
+
 int sdq_flux_attention(sdq_array *res, sdq_array qkv_a, sdq_array q_norm_a, sdq_array k_norm_a, sdq_array qkv_b,
                        sdq_array q_norm_b, sdq_array k_norm_b, sdq_array pe_cos, sdq_array pe_sin, int heads,
                        float scale, float eps, sdq_stream s) {
   SDQ_GUARD("flux_attention", {
-    const char *op = "flux_attention";
-    StreamImpl *st = stream_of(s, op);
+    StreamImpl *st = stream_of(s, "flux_attention");
     if (!res) fail("result pointer is NULL");
     constexpr int D = 128;
-    if (heads <= 0) fail("heads must be positive");
-    const int64_t width = int64_t(3) * heads * D;
-    struct Src {
-      ArrayImpl *x = nullptr;
-      const ArrayImpl *qn = nullptr, *kn = nullptr;
-      int n = 0;
-    } src[2];
-    sdq_array qkv[2] = {qkv_a, qkv_b}, qn[2] = {q_norm_a, q_norm_b}, kn[2] = {k_norm_a, k_norm_b};
-    for (int i = 0; i < 2; ++i) {
-      if (i == 1 && !qkv[1].ctx) break;
-      src[i].x = float_input(qkv[i], op, i ? "qkv_b" : "qkv_a", st);
-      const auto &sh = src[i].x->shape;
-      if (sh.size() != 3 || sh[2] < width)
-        fail("mlx: qkv got " + shape_str(sh) + "; need [batch, tokens, >= 3 * heads * 128]");
-      src[i].n = sh[1];
-      if (!qn[i].ctx || !kn[i].ctx) fail("the q and k norm scales are required");
-      src[i].qn = norm_param(qn[i], op, "query_norm.scale", D, st);
-      src[i].kn = norm_param(kn[i], op, "key_norm.scale", D, st);
-    }
-    const int B = src[0].x->shape[0];
-    if (src[1].x) {
-      if (src[1].x->shape[0] != B) fail("the two streams must have one batch size");
-      if (src[1].x->dtype != src[0].x->dtype) fail("the two streams must have one dtype");
-    }
-    const int wdt = src[0].qn->dtype;
-    for (int i = 0; i < 2; ++i)
-      if (src[i].x && (src[i].qn->dtype != wdt || src[i].kn->dtype != wdt))
-        fail("the norm scales must have one dtype");
-    const int N = src[0].n + src[1].n;
-    ArrayImpl *ca = float_input(pe_cos, op, "pe.cos", st);
-    ArrayImpl *sa = float_input(pe_sin, op, "pe.sin", st);
-    for (const ArrayImpl *p : {ca, sa}) {
-      if (p->dtype != SDQ_FLOAT32) fail("the rotary tables must be float32");
-      if (int64_t(p->size) != int64_t(N) * (D / 2))
-        fail("the rotary tables must hold [1, " + std::to_string(N) + ", 64] values, got " + shape_str(p->shape));
-    }
-    const int64_t ldt = kern::attention_vt_stride(N);
-    auto q = make_array({B, heads, N, D}, SDQ_BFLOAT16, *st);
-    auto k = make_array({B, heads, N, D}, SDQ_BFLOAT16, *st);
-    auto vt = make_array({B, heads, D, int(ldt)}, SDQ_BFLOAT16, *st);
-    kern::FluxPrepSrc pa, pb;
-    for (int i = 0; i < 2; ++i) {
-      if (!src[i].x) continue;
-      kern::FluxPrepSrc &p = i ? pb : pa;
-      p.qkv = src[i].x->data();
-      p.ld = src[i].x->shape[2];
-      p.sb = int64_t(src[i].n) * src[i].x->shape[2];
-      p.qn = src[i].qn->data();
-      p.kn = src[i].kn->data();
-    }
-    kern::flux_attention_prep(pa, pb, src[0].x->dtype, wdt, src[0].n, src[1].n, B, heads, eps,
-                              static_cast<const float *>(ca->data()), static_cast<const float *>(sa->data()),
-                              static_cast<uint16_t *>(q->data()), static_cast<uint16_t *>(k->data()),
-                              static_cast<uint16_t *>(vt->data()), ldt, st->stream);
+    const FluxAttnShape shp = flux_attention_shape(qkv_a, qkv_b, heads, st);
     // The output is merge_heads' layout, [batch, tokens, heads * 128].
-    auto out = make_array({B, N, heads * D}, src[0].x->dtype, *st);
-    kern::AttnArgs a;
-    a.q = static_cast<const uint16_t *>(q->data());
-    a.k = static_cast<const uint16_t *>(k->data());
-    a.vt = static_cast<const uint16_t *>(vt->data());
-    a.o = out->data();
-    a.q_sn = D, a.q_sh = int64_t(N) * D, a.q_sb = int64_t(heads) * N * D;
-    a.k_sn = D, a.k_sh = a.q_sh, a.k_sb = a.q_sb;
-    a.v_sd = ldt, a.v_sh = int64_t(D) * ldt, a.v_sb = int64_t(heads) * D * ldt;
-    a.o_sn = int64_t(heads) * D, a.o_sh = D, a.o_sb = int64_t(N) * heads * D;
-    a.B = B, a.H = heads, a.group = 1, a.Nq = N, a.Nk = N, a.D = D;
-    a.scale_log2 = scale * 1.4426950408889634f;
-    kern::attention(a, out->dtype, st->stream);
+    auto out = make_array({shp.B, shp.N, heads * D}, shp.dtype, *st);
+    flux_attention_into(out->data(), int64_t(heads) * D, qkv_a, q_norm_a, k_norm_a, qkv_b, q_norm_b, k_norm_b,
+                        pe_cos, pe_sin, heads, scale, eps, st);
     set_result(res, std::move(out));
   });
 }

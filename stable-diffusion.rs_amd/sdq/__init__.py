@@ -193,6 +193,12 @@ def _declare(L: ctypes.CDLL) -> None:
             [c_vp, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
              ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
         ),
+        "sdq_quantized_linear_split_raw": (
+            c_int,
+            [c_vp, ctypes.c_int64, c_int, c_vp, ctypes.c_int64, c_int, ctypes.c_int64, c_int, c_vp, c_int,
+             ctypes.c_int64, c_vp, c_vp, c_vp, c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int,
+             c_int, c_vp, c_int, c_vp],
+        ),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
         "sdq_gguf_dequantize": (c_int, [P(A), A, c_int, P(c_int), c_int, S]),
         "sdq_fast_layer_norm": (c_int, [P(A), A, A, A, ctypes.c_float, S]),
@@ -203,6 +209,9 @@ def _declare(L: ctypes.CDLL) -> None:
         "sdq_flux_rope": (c_int, [P(A), A, A, A, S]),
         "sdq_flux_attention": (
             c_int, [P(A), A, A, A, A, A, A, A, A, c_int, ctypes.c_float, ctypes.c_float, S]),
+        "sdq_flux_single_linear1_attention": (
+            c_int, [P(A), A, A, A, A, A, COptionalInt, COptionalInt, ctypes.c_char_p, A, A, A, A, c_int,
+                    ctypes.c_float, ctypes.c_float, S]),
         "sdq_gguf_quantize": (c_int, [P(V), A, c_int, P(c_int), c_int, COptionalInt, COptionalInt, S]),
         "sdq_array_device_ptr": (c_vp, [A]),
         "sdq_version": (ctypes.c_char_p, []),

@@ -20,7 +20,7 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-from . import Array, CArray, Stream, _check, _h, lib
+from . import Array, CArray, QuantizedArray, Stream, _check, _h, _some_int, lib
 
 EPS = 1e-6  # flux.rs:28
 
@@ -88,4 +88,24 @@ def attention(qkv: Array, query_norm: Array, key_norm: Array, pe: Rope, heads: i
                                     _h(query_norm2), _h(key_norm2), pe.cos._raw, pe.sin._raw, int(heads),
                                     float(scale), EPS, s._raw),
            "flux_attention")
+    return Array(out)
+
+
+def single_linear1_attention(x: Array, linear1: QuantizedArray, bias: Optional[Array], query_norm: Array,
+                             key_norm: Array, pe: Rope, heads: int, s: Stream,
+                             scale: Optional[float] = None) -> Array:
+    """The single block from its modulated input to linear2's input
+    (flux.rs:440-465): linear1, its q/k/v columns through the attention and
+    its MLP columns through GELU, concatenated as [attention, gelu(mlp)].  One
+    matmul launch writes the q/k/v columns to a buffer of their own and the
+    GELU'd MLP columns straight into the result; the attention then fills the
+    result's first heads * 128 columns."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(128)
+    out = CArray(None)
+    _check(lib().sdq_flux_single_linear1_attention(
+        ctypes.byref(out), x._raw, linear1.weight._raw, linear1.scales._raw, linear1.biases._raw, _h(bias),
+        _some_int(linear1.group_size), _some_int(linear1.bits), linear1.QUANT_MODE, query_norm._raw,
+        key_norm._raw, pe.cos._raw, pe.sin._raw, int(heads), float(scale), EPS, s._raw),
+        "flux_single_linear1_attention")
     return Array(out)
