@@ -239,10 +239,10 @@ typedef enum sdq_combine_ {
 /* sdq_quantized_linear followed by the combine stage above:
  * it replaces the mlx_multiply / mlx_add calls the reference issues after the
  * linear at those call sites.  residual: the output's shape, any float
- * dtype; gate: N values or a NULL-ctx handle.  For M <= 32 the whole
- * epilogue runs in the matmul's store, on the f32 value; for larger M the
- * combine stage runs as one in-place pass over the output right after the
- * matmul, on v rounded to the output dtype (as the unfused sequence does). */
+ * dtype; gate: N values or a NULL-ctx handle.  The whole epilogue runs in
+ * the matmul's store (or in the reduction of split-K tiles): for M <= 32 on
+ * the f32 value; for larger M the combine stage takes v rounded to the
+ * output dtype (as the unfused sequence does). */
 int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w,
                                  sdq_array scales, sdq_array biases,
                                  sdq_array bias, int activation,
@@ -250,6 +250,31 @@ int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w,
                                  int combine, sdq_optional_int group_size,
                                  sdq_optional_int bits, const char *mode,
                                  sdq_stream s);
+
+/* T5's gated feed-forward input, gelu_new(wi_0 x) * (wi_1 x) (t5.rs:201-214:
+ * the two linears, gelu_approx and mlx_multiply), in one matmul launch over
+ * both weights.  w/scales/biases: the two quantized weights with their rows
+ * interleaved in blocks of eight (sdq_pair_rows on each of the three arrays):
+ * 2 * N rows, N % 8 == 0.  y[..., N] = act(x @ gate.T + bias_g) * (x @ up.T +
+ * bias_u), computed in f32 from the accumulators and rounded once to y's
+ * dtype (the unfused sequence rounds after each of its four ops, so the two
+ * differ by output rounding steps).  bias: 2 * N values in the paired row
+ * order (sdq_pair_rows on the two biases), or a NULL-ctx handle; activation:
+ * applied to the gate, SDQ_ACT_GELU_APPROX for T5.  No mlx-c counterpart. */
+int sdq_quantized_linear_gated(sdq_array *res, sdq_array x, sdq_array w,
+                               sdq_array scales, sdq_array biases,
+                               sdq_array bias, int activation,
+                               sdq_optional_int group_size,
+                               sdq_optional_int bits, const char *mode,
+                               sdq_stream s);
+
+/* Rows of two equal-shaped arrays interleaved in blocks of eight: rows
+ * 16 b .. 16 b + 7 of the result are gate's rows 8 b .. 8 b + 7 and rows
+ * 16 b + 8 .. 16 b + 15 up's.  gate, up: the same shape [R, ...] (R a
+ * positive multiple of 8) and dtype; res: [2 R, ...].  It builds the operands
+ * of sdq_quantized_linear_gated once, at load time (packed weights, scales,
+ * biases and the optional bias alike).  No mlx-c counterpart. */
+int sdq_pair_rows(sdq_array *res, sdq_array gate, sdq_array up, sdq_stream s);
 
 /* ---- elementwise ops the linear and its callers use ------------------------- */
 
@@ -452,6 +477,19 @@ int sdq_quantized_linear_split_raw(void *y, int64_t ldy, int activation, void *y
                                    const void *biases, int s_dtype, int64_t M,
                                    int64_t N, int64_t K, int group_size, int bits,
                                    const void *bias, int bias_dtype, void *hip_stream);
+
+/* sdq_quantized_linear_gated on caller-owned device memory: y[M, N / 2] (row
+ * stride ldy elements, 0 = N / 2) from the paired weight w[N, K*bits/32]
+ * (N % 16 == 0, rows as sdq_pair_rows lays them out); bias: N values in the
+ * paired order, or NULL.  Other arguments as
+ * sdq_quantized_matmul_epilogue_raw. */
+int sdq_quantized_linear_gated_raw(void *y, int64_t ldy, int y_dtype,
+                                   const void *x, int x_dtype, int64_t ldx,
+                                   const uint32_t *w, const void *scales,
+                                   const void *biases, int s_dtype, int64_t M,
+                                   int64_t N, int64_t K, int group_size,
+                                   int bits, const void *bias, int bias_dtype,
+                                   int activation, void *hip_stream);
 
 /* tanh-GELU on caller-owned device memory (dtype float32/bfloat16/float16),
  * enqueued on `hip_stream`: the elementwise step between the two Flux MLP

@@ -58,6 +58,13 @@ void gguf_quantize(const uint8_t *raw, int type, int64_t rows, int64_t cols, int
 // q/k/v columns to one buffer, its GELU'd MLP columns into linear2's input
 // after the attention output, flux.rs:440-469).  No combine stage with a
 // split.
+//
+// Gated pair (pair = 1): the weight's rows come in blocks of 16, eight rows
+// of a gate projection then the matching eight of an up projection
+// (quantize_pair); output column 8 b + i (of N / 2) is
+// act(v[16 b + i]) * v[16 b + 8 + i], v = acc + bias: T5's
+// gelu(wi_0 x) * (wi_1 x) (t5.rs:209-214) in one launch.  No split or
+// combine stage with a pair; ldy applies to the N / 2 output columns.
 struct Epilogue {
   const void *bias = nullptr;
   int bias_dtype = 0;
@@ -73,6 +80,7 @@ struct Epilogue {
   void *y2 = nullptr;
   int64_t ldy2 = 0;
   int act2 = 0;
+  int pair = 0;
 };
 
 inline bool epi_dtype_ok(int dt) {
@@ -88,6 +96,7 @@ inline bool epilogue_ok(const Epilogue &ep) {
     if (ep.act2 != 0 && ep.act2 != 1) return false;
     if (ep.combine != 0) return false;
   }
+  if (ep.pair != 0 && (ep.pair != 1 || ep.split != 0 || ep.combine != 0)) return false;
   if (ep.combine == 0) return true;
   if (ep.combine != 1 && ep.combine != 2) return false;
   if (!ep.res || !epi_dtype_ok(ep.res_dtype)) return false;

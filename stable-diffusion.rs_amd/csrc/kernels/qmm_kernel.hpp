@@ -419,14 +419,19 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   const bool comb_vec = comb && a16(ep.res) && (ep.ld_res * int64_t(dtype_size_dev(ep.res_dtype))) % 16 == 0 &&
                         (!ep.gate || a16(ep.gate));
-  auto store_tile = [&](auto produce) {
+  // PAIR (kern::Epilogue::pair): `produce` leaves each gate column's
+  // product in the gate lanes; the pieces of up columns are not stored and a
+  // gate piece goes to output column (c / 16) * 8 + c % 8 of the wave's 32.
+  auto store_tile = [&](auto produce, auto pairc) {
+    constexpr bool PAIR = decltype(pairc)::value;
     // Output layout (kern::Epilogue): a tile lies wholly on one side of the
     // split (a multiple of 256).
     const bool hi = ep.split > 0 && nw - wave * 64 >= ep.split;
     OT *const ybase = hi ? static_cast<OT *>(ep.y2) : y;
-    const int64_t ldo = hi ? ep.ldy2 : (ep.ldy > 0 ? ep.ldy : int64_t(N));
+    const int nout = PAIR ? N / 2 : N;
+    const int64_t ldo = hi ? ep.ldy2 : (ep.ldy > 0 ? ep.ldy : int64_t(nout));
     const int col0 = hi ? int(ep.split) : 0;
-    const bool vec = N % kChunkElems == 0 && a16(ybase) && (ldo * int64_t(sizeof(OT))) % 16 == 0;
+    const bool vec = nout % kChunkElems == 0 && a16(ybase) && (ldo * int64_t(sizeof(OT))) % 16 == 0;
     uint8_t *wl = reinterpret_cast<uint8_t *>(xs) + wave * kWaveLds;
 #pragma unroll
     for (int p0 = 0; p0 < MB; p0 += kPassMB) {
@@ -456,11 +461,16 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
         const int row = idx / kCpr, chunk = idx % kCpr;
         u32x4 v = *reinterpret_cast<const u32x4 *>(wl + row * kRowBytes + chunk * 16);
         const int grow = m0 + 32 * p0 + row;
-        const int gcol = nw + chunk * kChunkElems;
+        int gcol = nw + chunk * kChunkElems;
+        if constexpr (PAIR) {
+          const int c = chunk * kChunkElems; // slab column of the piece's first element
+          if ((c & 8) != 0) return;          // an up piece
+          gcol = nw / 2 + (c >> 4) * 8 + (c & 7);
+        }
         if (grow >= M) return;
         OT *dst = ybase + int64_t(grow) * ldo + (gcol - col0);
         if constexpr (decltype(cb)::value) {
-          if (gcol < N) {
+          if (gcol < nout) {
             // Whole chunk in range (vec) or the ragged last one (elementwise).
             float f[kChunkElems];
 #pragma unroll
@@ -474,7 +484,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
             } else {
 #pragma unroll
               for (int q = 0; q < kChunkElems; ++q)
-                if (gcol + q < N) f[q] = epi_combine(ep, f[q], grow, gcol + q);
+                if (gcol + q < nout) f[q] = epi_combine(ep, f[q], grow, gcol + q);
             }
 #pragma unroll
             for (int q = 0; q < kChunkElems; ++q) {
@@ -489,12 +499,12 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
           }
         }
         if (vec) {
-          if (gcol < N) *reinterpret_cast<u32x4 *>(dst) = v;
+          if (gcol < nout) *reinterpret_cast<u32x4 *>(dst) = v;
         } else {
           // Rows not 16-byte aligned, or a ragged last chunk: element stores.
 #pragma unroll
           for (int q = 0; q < kChunkElems; ++q) {
-            if (gcol + q < N) {
+            if (gcol + q < nout) {
               const uint32_t word = v[(q * int(sizeof(OT))) / 4];
               if constexpr (sizeof(OT) == 4)
                 dst[q] = __builtin_bit_cast(OT, word);
@@ -505,9 +515,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
         }
       };
       constexpr int kPieces = kPassMB * 32 * kCpr / 64;
-      if (comb) {
+      if (!PAIR && comb) {
 #pragma unroll 1
-        for (int it = 0; it < kPieces; ++it) readback(it, std::integral_constant<bool, true>{});
+        for (int it = 0; it < kPieces; ++it) readback(it, std::integral_constant<bool, !PAIR>{});
       } else {
 #pragma unroll
         for (int it = 0; it < kPieces; ++it) readback(it, std::integral_constant<bool, false>{});
@@ -577,20 +587,33 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
     float bcol[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) bcol[j] = epi_bias(ep, min(nw + 32 * j + r, N - 1));
-    auto finish = [&](auto act) {
+    // PAIR: lane r holds gate column r when (r & 8) == 0 and the matching up
+    // column in lane r + 8 (rows interleaved in blocks of eight).
+    auto finish = [&](auto act, auto pairc) {
       store_tile([&](int mb, int j, float (&v)[16]) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const float t = acc[mb][j][e] + bcol[j];
-          v[e] = decltype(act)::value ? gelu_approx_f(t) : t;
+          const float a = decltype(act)::value ? gelu_approx_f(t) : t;
+          if constexpr (decltype(pairc)::value)
+            v[e] = a * __shfl_xor(t, 8);
+          else
+            v[e] = a;
         }
-      });
+      }, pairc);
     };
     const bool hi = ep.split > 0 && nw - wave * 64 >= ep.split;
-    if ((hi ? ep.act2 : ep.act) == 1)
-      finish(std::integral_constant<bool, true>{});
-    else
-      finish(std::integral_constant<bool, false>{});
+    const bool gelu = (hi ? ep.act2 : ep.act) == 1;
+    if (ep.pair) {
+      if (gelu)
+        finish(std::integral_constant<bool, true>{}, std::integral_constant<bool, true>{});
+      else
+        finish(std::integral_constant<bool, false>{}, std::integral_constant<bool, true>{});
+    } else if (gelu) {
+      finish(std::integral_constant<bool, true>{}, std::integral_constant<bool, false>{});
+    } else {
+      finish(std::integral_constant<bool, false>{}, std::integral_constant<bool, false>{});
+    }
   };
 
   // Data-parallel launch (sk_workers == 0): block b computes tile b whole,
@@ -744,24 +767,44 @@ __global__ __launch_bounds__(256) void qmm_reduce_kernel(typename Elem<ODT>::T *
   const int grow = tm * bm + row;
   const int gcol = tn * kTileN + col;
   if (grow >= M || gcol >= N) return;
-  const float4 *src = reinterpret_cast<const float4 *>(partial) + int64_t(sk) * splits * per_tile + within;
-  float4 sum = src[0];
-  for (int p0 = 1; p0 < splits; p0 += 4) {
-    float4 v[4];
+  // Gated pair: the thread of a gate column also sums the matching up column
+  // (eight columns on: the partial layout's thread t + 8); up columns' threads
+  // have nothing to store.
+  if (ep.pair && (gcol & 8)) return;
+  auto sum_of = [&](int64_t w) {
+    const float4 *src = reinterpret_cast<const float4 *>(partial) + int64_t(sk) * splits * per_tile + w;
+    float4 sum = src[0];
+    for (int p0 = 1; p0 < splits; p0 += 4) {
+      float4 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (p0 + u < splits) v[u] = src[int64_t(p0 + u) * per_tile];
+      for (int u = 0; u < 4; ++u)
+        if (p0 + u < splits) v[u] = src[int64_t(p0 + u) * per_tile];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (p0 + u < splits) {
-        sum.x += v[u].x;
-        sum.y += v[u].y;
-        sum.z += v[u].z;
-        sum.w += v[u].w;
-      }
-  }
+      for (int u = 0; u < 4; ++u)
+        if (p0 + u < splits) {
+          sum.x += v[u].x;
+          sum.y += v[u].y;
+          sum.z += v[u].z;
+          sum.w += v[u].w;
+        }
+    }
+    return sum;
+  };
+  const float4 sum = sum_of(within);
   const float b = epi_bias(ep, gcol);
   const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+  if (ep.pair) {
+    const float4 up = sum_of(within + 8);
+    const float bu = epi_bias(ep, gcol + 8);
+    const float u4[4] = {up.x, up.y, up.z, up.w};
+    const int ocol = (gcol >> 4) * 8 + (gcol & 7);
+    const int64_t ldo = ep.ldy > 0 ? ep.ldy : int64_t(N / 2);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (grow + u < M)
+        y[int64_t(grow + u) * ldo + ocol] = Elem<ODT>::store(epi_apply(ep, s4[u], b) * (u4[u] + bu));
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < 4; ++u)
     if (grow + u < M) {

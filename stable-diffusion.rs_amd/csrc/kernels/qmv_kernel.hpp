@@ -533,8 +533,24 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
 
   // Accumulator entry e of lane (n, h) in row block mb is token
   // 16 mb + 4 h + e, output column n of the tile.
-  if (!live || n >= N) return;
+  if (!live) return;
   const float bn = epi_bias(ep, n);
+  if (ep.pair) {
+    // Gated pair (kern::Epilogue::pair, N % 16 == 0): column ln < 8 of the
+    // tile is a gate, ln + 8 (lane ^ 8) its up column; output column
+    // 8 tile + ln of N / 2.
+    const int64_t ldo = ep.ldy > 0 ? ep.ldy : int64_t(N / 2);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float up = __shfl_xor(acc[mb][e] + bn, 8);
+        const int m = mb * 16 + 4 * lh + e;
+        if (ln < 8 && m < M) y[m * ldo + tile * 8 + ln] = Elem<ODT>::store(epi_apply(ep, acc[mb][e], bn) * up);
+      }
+    return;
+  }
+  if (n >= N) return;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll

@@ -60,7 +60,13 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
                      int s_dtype, int64_t M, int64_t N, int64_t K, int gs, int bits,
                      int device, hipStream_t stream, const kern::Epilogue &ep) {
   if (M == 0 || N == 0) return;
-  if (ep.split != 0) {
+  if (ep.pair != 0) {
+    if (N % 16 != 0)
+      fail("a gated pair's weight has rows in blocks of sixteen (eight gate, eight up), got N = " +
+           std::to_string(N));
+    if (ep.split != 0 || ep.combine != 0) fail("a gated pair takes no output split or combine stage");
+    if (ep.ldy != 0 && ep.ldy < N / 2) fail("the output row stride is shorter than N / 2");
+  } else if (ep.split != 0) {
     if (ep.split % 256 != 0 || ep.split <= 0 || ep.split >= N)
       fail("the output split must be a multiple of 256 inside (0, N), got " + std::to_string(ep.split) +
            " for N = " + std::to_string(N));
@@ -280,7 +286,8 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
                            sdq_array biases, bool transpose, sdq_optional_int group_size,
                            sdq_optional_int bits, const char *mode, sdq_stream s,
                            sdq_array bias, int activation, sdq_array residual = sdq_array{nullptr},
-                           sdq_array gate = sdq_array{nullptr}, int combine = SDQ_COMBINE_NONE) {
+                           sdq_array gate = sdq_array{nullptr}, int combine = SDQ_COMBINE_NONE,
+                           bool pair = false) {
     StreamImpl *st = stream_of(s, "quantized_matmul");
     if (!transpose)
       fail("transpose=false (x @ W with W quantized along its output axis) is not "
@@ -324,6 +331,12 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
       fail("a residual or gate was given without a combine mode");
     }
     ep.combine = combine;
+    if (pair) {
+      if (N % 16 != 0)
+        fail("a gated pair's weight has rows in blocks of sixteen (eight gate, eight up; sdq_pair_rows), "
+             "got " + std::to_string(N) + " rows");
+      ep.pair = 1;
+    }
     const int out_dtype = promote_float(xa->dtype, sa->dtype);
     if (bb) order_after(bb, st);
     if (ra) order_after(ra, st);
@@ -333,7 +346,7 @@ void quantized_matmul_impl(sdq_array *res, sdq_array x, sdq_array w, sdq_array s
     order_after(sa, st);
     order_after(ba, st);
     std::vector<int> oshape = xa->shape;
-    oshape.back() = int(N);
+    oshape.back() = int(pair ? N / 2 : N);
     auto out = make_array(oshape, out_dtype, *st);
     const int64_t M = K ? int64_t(xa->size / size_t(K)) : 0;
     matmul_dispatch(out->data(), out_dtype, xa->data(), xa->dtype, K,
@@ -377,6 +390,84 @@ int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w, sdq_a
 }
 
 
+
+int sdq_quantized_linear_gated(sdq_array *res, sdq_array x, sdq_array w, sdq_array scales,
+                               sdq_array biases, sdq_array bias, int activation,
+                               sdq_optional_int group_size, sdq_optional_int bits, const char *mode,
+                               sdq_stream s) {
+  SDQ_GUARD("quantized_linear_gated", {
+    quantized_matmul_impl(res, x, w, scales, biases, true, group_size, bits, mode, s, bias,
+                          activation, sdq_array{nullptr}, sdq_array{nullptr}, SDQ_COMBINE_NONE, true);
+  });
+}
+
+int sdq_pair_rows(sdq_array *res, sdq_array gate, sdq_array up, sdq_stream s) {
+  SDQ_GUARD("pair_rows", {
+    StreamImpl *st = stream_of(s, "pair_rows");
+    if (!res) fail("result pointer is NULL");
+    ArrayImpl *ga = array_of(gate, "pair_rows", "gate");
+    ArrayImpl *ua = array_of(up, "pair_rows", "up");
+    same_device(ga, st, "gate");
+    same_device(ua, st, "up");
+    if (ga->shape != ua->shape || ga->dtype != ua->dtype)
+      fail("gate and up must share one shape and dtype, got " + shape_str(ga->shape) + " " +
+           dtype_name(ga->dtype) + " and " + shape_str(ua->shape) + " " + dtype_name(ua->dtype));
+    if (ga->shape.empty() || ga->shape[0] % 8 != 0 || ga->shape[0] <= 0)
+      fail("pair_rows takes arrays whose first dimension is a positive multiple of 8, got " +
+           shape_str(ga->shape));
+    const int64_t rows = ga->shape[0];
+    const size_t row_bytes = ga->nbytes() / size_t(rows);
+    std::vector<int> oshape = ga->shape;
+    oshape[0] = int(2 * rows);
+    order_after(ga, st);
+    order_after(ua, st);
+    auto out = make_array(oshape, ga->dtype, *st);
+    // Blocks of eight rows: gate's block b to result rows 16 b.., up's to
+    // 16 b + 8.. -- two strided copies.
+    if (row_bytes > 0) {
+      unsigned char *dst = static_cast<unsigned char *>(out->data());
+      const size_t blk = 8 * row_bytes;
+      hip_check(hipMemcpy2DAsync(dst, 2 * blk, ga->data(), blk, blk, size_t(rows / 8),
+                                 hipMemcpyDeviceToDevice, st->stream),
+                "hipMemcpy2DAsync");
+      hip_check(hipMemcpy2DAsync(dst + blk, 2 * blk, ua->data(), blk, blk, size_t(rows / 8),
+                                 hipMemcpyDeviceToDevice, st->stream),
+                "hipMemcpy2DAsync");
+    }
+    set_result(res, std::move(out));
+  });
+}
+
+int sdq_quantized_linear_gated_raw(void *y, int64_t ldy, int y_dtype, const void *x, int x_dtype,
+                                   int64_t ldx, const uint32_t *w, const void *scales, const void *biases,
+                                   int s_dtype, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                   const void *bias, int bias_dtype, int activation, void *hip_stream) {
+  SDQ_GUARD("quantized_linear_gated_raw", {
+    if (M < 0 || N < 0 || K <= 0) fail("M, N must be >= 0 and K > 0");
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(s_dtype) || !is_float_dtype(y_dtype))
+      fail("dtypes must be float32, bfloat16 or float16");
+    if (bias && !is_float_dtype(bias_dtype))
+      fail("bias dtype must be float32, bfloat16 or float16");
+    if (activation != SDQ_ACT_NONE && activation != SDQ_ACT_GELU_APPROX)
+      fail("activation must be SDQ_ACT_NONE or SDQ_ACT_GELU_APPROX, got " + std::to_string(activation));
+    check_group_bits(group_size, bits);
+    if (K % group_size != 0) fail("K must be a multiple of group_size");
+    if (N % 16 != 0) fail("N (the paired weight's rows) must be a multiple of 16, got " + std::to_string(N));
+    if (ldy < 0) fail("negative output row stride");
+    if (M > 0 && N > 0 && (!y || !x || !w || !scales || !biases)) fail("NULL pointer argument");
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    kern::Epilogue ep;
+    ep.bias = bias;
+    ep.bias_dtype = bias ? bias_dtype : 0;
+    ep.act = activation;
+    ep.ldy = ldy;
+    ep.pair = 1;
+    if (!kern::epilogue_ok(ep)) fail("bad epilogue");
+    matmul_dispatch(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K,
+                    group_size, bits, device, static_cast<hipStream_t>(hip_stream), ep);
+  });
+}
 
 int sdq_quantized_matmul_raw(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
                              const uint32_t *w, const void *scales, const void *biases,

@@ -199,6 +199,16 @@ def _declare(L: ctypes.CDLL) -> None:
              ctypes.c_int64, c_vp, c_vp, c_vp, c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int,
              c_int, c_vp, c_int, c_vp],
         ),
+        "sdq_quantized_linear_gated_raw": (
+            c_int,
+            [c_vp, ctypes.c_int64, c_int, c_vp, c_int, ctypes.c_int64, c_vp, c_vp, c_vp, c_int,
+             ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_int, c_int, c_vp, c_int, c_int, c_vp],
+        ),
+        "sdq_quantized_linear_gated": (
+            c_int,
+            [P(A), A, A, A, A, A, c_int, COptionalInt, COptionalInt, ctypes.c_char_p, S],
+        ),
+        "sdq_pair_rows": (c_int, [P(A), A, A, S]),
         "sdq_gelu_approx_raw": (c_int, [c_vp, c_vp, c_int, ctypes.c_int64, c_vp]),
         "sdq_gguf_dequantize": (c_int, [P(A), A, c_int, P(c_int), c_int, S]),
         "sdq_fast_layer_norm": (c_int, [P(A), A, A, A, ctypes.c_float, S]),
@@ -641,6 +651,31 @@ class QuantizedArray:
         )
         return Array(res)
 
+    @classmethod
+    def pair(cls, gate: "QuantizedArray", up: "QuantizedArray", stream: Stream) -> "QuantizedArray":
+        """The operand of `linear_gated`: gate's and up's rows interleaved in
+        blocks of eight (packed weights, scales and biases alike), built once
+        at load time from T5's wi_0 and wi_1 (t5.rs:209-214)."""
+        if (gate.group_size, gate.bits) != (up.group_size, up.bits):
+            raise Error("pair: gate and up must share group size and bits")
+        return cls(pair_rows(gate.weight, up.weight, stream), pair_rows(gate.scales, up.scales, stream),
+                   pair_rows(gate.biases, up.biases, stream), gate.group_size, gate.bits)
+
+    def linear_gated(self, x: Array, stream: Stream, bias: Array | None = None,
+                     activation: int = ACT_GELU_APPROX) -> Array:
+        """act(x @ gate.T + bias_g) * (x @ up.T + bias_u) in one launch, this
+        array being a `pair`: T5's gelu_new(wi_0 x) * (wi_1 x)
+        (t5.rs:201-214).  bias: the two biases through `pair_rows`."""
+        res = CArray(None)
+        _check(
+            lib().sdq_quantized_linear_gated(ctypes.byref(res), x._raw, self.weight._raw,
+                                             self.scales._raw, self.biases._raw, _h(bias),
+                                             int(activation), _some_int(self.group_size),
+                                             _some_int(self.bits), self.QUANT_MODE, stream._raw),
+            "quantized_linear_gated",
+        )
+        return Array(res)
+
     def resident_bytes(self) -> int:
         """Packed words at 4 bytes plus scales and biases at 4 bytes each, the
         reference's accounting (mlx.rs:1977-1985)."""
@@ -655,6 +690,15 @@ class QuantizedArray:
 def _h(a: "Array | None") -> CArray:
     """An optional array argument: the handle, or an empty one."""
     return CArray(None) if a is None else a._raw
+
+
+def pair_rows(gate: Array, up: Array, stream: Stream) -> Array:
+    """Rows of two equal-shaped arrays interleaved in blocks of eight (gate's
+    block b at rows 16 b.., up's at 16 b + 8..): the layout `linear_gated`
+    reads."""
+    res = CArray(None)
+    _check(lib().sdq_pair_rows(ctypes.byref(res), gate._raw, up._raw, stream._raw), "pair_rows")
+    return Array(res)
 
 
 def _raw_bytes(raw) -> Array:
