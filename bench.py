@@ -140,7 +140,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU baseline work")
     ap.add_argument("--unfused", action="store_true",
                     help="report the unfused form (fc1, GELU kernel, fc2) as the headline")
-    ap.add_argument("--only", choices=["step", "sweep", "config5"], default=None,
+    ap.add_argument("--no-config3", action="store_true")
+    ap.add_argument("--only", choices=["step", "sweep", "config3", "config5"], default=None,
                     help="run one part only (for profiling its kernels)")
     ap.add_argument("--sweep-m", default="1,4,16,32,64,128,256,512,1024,1536,4608",
                     help="comma-separated M values of the 3072->12288 sweep")
@@ -169,6 +170,14 @@ class Raw:
                                                  M, N, K, GS, bits, hs)
         if rc:
             sdq._check(rc, "quantized_matmul_raw")
+
+    def gated(self, y, x, w, s, b, M, N2, K, bits, hs):
+        """T5's gelu(wi_0 x) * (wi_1 x) from the paired weight (N2 rows)."""
+        sdq = self.sdq
+        rc = self.L.sdq_quantized_linear_gated_raw(y, 0, sdq.BFLOAT16, x, sdq.BFLOAT16, K, w, s, b, sdq.FLOAT32,
+                                                   M, N2, K, GS, bits, None, 0, sdq.ACT_GELU_APPROX, hs)
+        if rc:
+            sdq._check(rc, "quantized_linear_gated_raw")
 
     def gelu(self, out, inp, n, hs):
         rc = self.L.sdq_gelu_approx_raw(out, inp, self.sdq.BFLOAT16, n, hs)
@@ -253,6 +262,85 @@ def graph_time(torch, raw, layer, M, x, y, reps=6):
         raise RuntimeError(f"graph replay of M={M} N={layer.N} K={layer.K} differs from the eager launch")
     del g
     return best
+
+
+def graph_time_fn(torch, launch, nrot, reps=6):
+    """Per-iteration ms of `launch(i, hip_stream)` for i in range(nrot) (one
+    weight copy each), captured in one HIP graph and replayed `reps` times;
+    the minimum replay."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(2 * nrot):
+            launch(i % nrot, s.cuda_stream)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(nrot):
+            launch(i, s.cuda_stream)
+    best = float("inf")
+    with torch.cuda.stream(s):
+        for r in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+            e1.synchronize()
+            if r > 0:
+                best = min(best, e0.elapsed_time(e1) / nrot)
+    s.synchronize()
+    del g
+    return best
+
+
+def config3(torch, raw, sdq, dev, g):
+    """BASELINE config 3, T5-XXL's gated-GELU FFN (t5.rs:201-214): wi_0 and
+    wi_1 4096->10240 4-bit, wo 10240->4096 8-bit, at M = 512 and the GEMV
+    sweep M = 1, 4, 16.  Two forms of the FFN input are timed: the paired
+    weight in one launch (sdq_quantized_linear_gated_raw), and the reference's
+    sequence with the GELU fused into wi_0's epilogue -- wi_0+GELU, wi_1, an
+    elementwise product -- each as HIP-graph replays over rotated weights."""
+    D, F = 4096, 10240
+    pair = SynthLayer(torch, dev, 2 * F, D, 4, seed=31)
+    wi0 = SynthLayer(torch, dev, F, D, 4, seed=32)
+    wi1 = SynthLayer(torch, dev, F, D, 4, seed=33)
+    wo = SynthLayer(torch, dev, D, F, 8, seed=34)
+    x = torch.randn(512, D, device=dev, generator=g).to(torch.bfloat16)
+    hg = torch.empty(512, F, device=dev, dtype=torch.bfloat16)
+    hu = torch.empty_like(hg)
+    a = torch.empty_like(hg)
+    y = torch.empty(512, D, device=dev, dtype=torch.bfloat16)
+    rows = []
+    for M in (512, 1, 4, 16):
+        def gated(i, hs):
+            w, sc, b = pair.ptrs[i]
+            raw.gated(a.data_ptr(), x.data_ptr(), w, sc, b, M, 2 * F, D, 4, hs)
+
+        def two(i, hs):
+            w, sc, b = wi0.ptrs[i % wi0.rotate]
+            raw.matmul(hg.data_ptr(), x.data_ptr(), w, sc, b, M, F, D, 4, hs, act=sdq.ACT_GELU_APPROX)
+            w, sc, b = wi1.ptrs[i % wi1.rotate]
+            raw.matmul(hu.data_ptr(), x.data_ptr(), w, sc, b, M, F, D, 4, hs)
+            torch.mul(hg[:M], hu[:M], out=a[:M])
+
+        def out(i, hs):
+            w, sc, b = wo.ptrs[i]
+            raw.matmul(y.data_ptr(), a.data_ptr(), w, sc, b, M, D, F, 8, hs)
+
+        t_gated = graph_time_fn(torch, gated, pair.rotate)
+        t_two = graph_time_fn(torch, two, max(wi0.rotate, wi1.rotate))
+        t_wo = graph_time_fn(torch, out, wo.rotate)
+        pt = roofline_point(M, 2 * F, D, 4, t_gated)
+        rows.append({"M": M, "ms_gated_pair": round(t_gated, 4), "ms_wi0_gelu_wi1_mul": round(t_two, 4),
+                     "ms_wo": round(t_wo, 4), "ms_ffn": round(t_gated + t_wo, 4),
+                     "ms_ffn_two_linear_form": round(t_two + t_wo, 4),
+                     "gated_pair_roofline": {k: pt[k] for k in ("TFLOP/s", "GB/s", "bound", "frac")}})
+        log(f"config3 T5 FFN M={M:4d}: gated pair {t_gated * 1e3:8.2f} us ({pt['bound']} {pt['frac'] * 100:5.1f}%), "
+            f"wi_0+gelu, wi_1, mul {t_two * 1e3:8.2f} us; wo {t_wo * 1e3:8.2f} us; "
+            f"FFN {(t_gated + t_wo) * 1e3:8.2f} vs {(t_two + t_wo) * 1e3:8.2f} us")
+    del pair, wi0, wi1, wo, x, hg, hu, a, y
+    return {"note": "T5-XXL FFN (d_model 4096, d_ff 10240; wi 4-bit, wo 8-bit, group 64): the paired gated "
+                    "launch vs wi_0 with the GELU epilogue + wi_1 + an elementwise product; HIP-graph replays "
+                    "over device-random weights rotated through > 512 MB", "points": rows}
 
 
 def cpu_baseline(args, fc1, fc2):
@@ -451,6 +539,11 @@ def main():
             del layer
         del xs, ys
 
+    # ---- config 3: T5-XXL's gated FFN ------------------------------------------------------------
+    c3 = None
+    if args.only in (None, "config3") and not args.no_config3:
+        c3 = config3(torch, raw, sdq, dev, g)
+
     # ---- config 5: one Flux-schnell step's quantized linears ------------------------------------
     config5 = None
     if args.only in (None, "config5") and not args.no_config5:
@@ -537,6 +630,7 @@ def main():
         **{k: v for k, v in rec_step.items() if k not in ("value", "ms_per_step")},
         "cpu_baseline": cpu,
         "sweep_3072x12288": sweep,
+        "config3": c3,
         "config5": config5,
     }
     print(json.dumps(rec), flush=True)

@@ -120,16 +120,23 @@ struct QmvPlan {
   int waves = 4;           // S: K ranges per tile (the block has T * S waves)
   int row_blocks = 1;      // 16-token MFMA row blocks: 1 for M <= 16, 2 for M <= 32
   int xmode = 1;           // where x comes from: 0 read per chunk, 1 staged per
-                           // wave, 2 staged once per block
+                           // wave, 2 staged once per block, 3 a K range
+                           // staged per block (ranges > 1 blocks per tile)
+  int ranges = 1;          // R: K ranges across blocks (xmode 3)
   int lds_bytes = 0;       // dynamic LDS of one block
+  size_t partial_floats = 0; // workspace for the ranges' partial tiles
 };
 
-// y [M, N] = x [M, K] @ dequantize(w).T for M <= 32.  qmv.hip.
-QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus);
+// y [M, N] = x [M, K] @ dequantize(w).T for M <= 32.  qmv.hip.  With
+// allow_split false the plan needs no workspace (ranges == 1).
+QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus,
+                 bool allow_split = true);
+// partial: plan.partial_floats floats of workspace when plan.ranges > 1.
 void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream);
+         int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream,
+         float *partial = nullptr);
 
 // Tile and split-K plan of one qmm launch (a pure function of the shape and
 // the CU count).

@@ -16,7 +16,7 @@ namespace qmv_detail {
 template <int XD, int SD, int OD>
 void qmv_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
                const void *b, int M, int N, int K, int gs, const kern::QmvPlan &plan,
-               const kern::Epilogue &ep, hipStream_t st);
+               const kern::Epilogue &ep, hipStream_t st, float *partial);
 
 } // namespace qmv_detail
 
@@ -28,7 +28,7 @@ constexpr int kLdsMax = 150 * 1024;       // of the CU's 160 KB
 #define SDQ_QMV_CASE(XD, SD, OD)                                                              \
   if (x_dtype == XD && s_dtype == SD && y_dtype == OD) {                                      \
     qmv_detail::qmv_combo<XD, SD, OD>(bits, y, x, ldx, w, scales, biases, int(M), int(N), int(K), \
-                                      group_size, plan, ep, stream);                          \
+                                      group_size, plan, ep, stream, partial);                 \
     hip_check(hipGetLastError(), "qmv launch");                                               \
     return;                                                                                   \
   }
@@ -37,8 +37,7 @@ constexpr int kLdsMax = 150 * 1024;       // of the CU's 160 KB
 
 namespace kern {
 
-QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus) {
-  (void)bits;
+QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus, bool allow_split) {
   using namespace qmv_detail;
   QmvPlan p;
   p.row_blocks = M <= 16 ? 1 : 2;
@@ -82,6 +81,52 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
       return p;
     }
   }
+  // A large x: K in R ranges, each staged once per block of T tiles.  The
+  // shape is chosen by an estimate of the busiest CU's time, in 128-wide
+  // chunks of one tile's codes: its blocks' code chunks, their x slices
+  // (read from L2, weighted 1/4) and partial tiles, slowed in proportion
+  // when fewer than eight waves stream on it.  R: the fewest ranges whose
+  // slice of x fits, or one more.
+  if (allow_split && M > 4) {
+    double best_cost = 0.0;
+    int bestR = 0, bestT = 0, bestS = 0;
+    int rmin = 0;
+    for (int R = 2; R <= kMaxRanges && R <= nchunk; ++R) {
+      const int64_t nb = (nchunk + R - 1) / R;
+      if (M * (nb * 128 + 8) * 2 > kStageXMax) continue;
+      if (!rmin) rmin = R;
+      if (R > rmin + 1) break;
+      for (int T = 16; T >= 1; --T) {
+        for (int S = 1; T * S <= kMaxWaves[kXSplit] && S <= nb; ++S) {
+          const QmvLds l = qmv_lds(kXSplit, int(M), int(K), group_size, T, S, p.row_blocks, R);
+          if (l.total > kLdsMax) break;
+          const int64_t blocks = (tiles + T - 1) / T * R;
+          const int64_t per_cu = std::min<int64_t>(kLdsMax / l.total, 32 / (T * S));
+          const int64_t load = (blocks + ncu - 1) / ncu; // blocks on the busiest CU
+          const int64_t active = std::min(per_cu, load) * T * S;
+          const double x_chunks = 0.25 * double(M) / bits;       // per chunk of K, per block
+          const double part = double(R) * M * 16 * 8 / (256.0 * bits); // per tile
+          const double cost = double(load) * (double(nb) * (T + x_chunks) + T * part) *
+                              std::max(1.0, 8.0 / double(active));
+          if (!bestR || cost < best_cost - 1e-9) {
+            best_cost = cost;
+            bestR = R;
+            bestT = T;
+            bestS = S;
+          }
+        }
+      }
+    }
+    if (bestR) {
+      p.xmode = kXSplit;
+      p.ranges = bestR;
+      p.tiles_per_block = bestT;
+      p.waves = bestS;
+      p.lds_bytes = qmv_lds(kXSplit, int(M), int(K), group_size, bestT, bestS, p.row_blocks, bestR).total;
+      p.partial_floats = size_t(bestR) * size_t(tiles) * size_t(p.row_blocks) * 64 * 4;
+      return p;
+    }
+  }
   p.xmode = kXDirect;
   p.tiles_per_block = 1;
   p.waves = waves_for(1, kMaxWaves[kXDirect]);
@@ -93,7 +138,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
 void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
-         int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream) {
+         int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream, float *partial) {
   if (M < 1 || M > 32) fail("qmv: M must be in [1, 32]");
   if (N < 1 || K < 64 || K % 64 != 0) fail("qmv: bad N or K");
   if (group_size != 64 && group_size != 128) fail("qmv: group size must be 64 or 128");
@@ -107,14 +152,23 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
       N * (K / group_size) * int64_t(dtype_size(s_dtype)) >= lim)
     fail("qmv: x, the packed weight, scales and biases must each be under 2 GiB");
   if (plan.row_blocks != (M <= 16 ? 1 : 2)) fail("qmv: plan's row blocks do not cover M");
-  if ((K / 128 + 1) * int64_t(plan.waves + 1) >= lim) fail("qmv: K too large for the chunk arithmetic");
   using namespace qmv_detail;
-  if (plan.xmode < kXDirect || plan.xmode > kXBlock || plan.tiles_per_block < 1 || plan.waves < 1 ||
+  if ((K / 128 + 1) * int64_t(std::max(plan.waves, kMaxRanges) + 1) >= lim)
+    fail("qmv: K too large for the chunk arithmetic");
+  if (plan.xmode < kXDirect || plan.xmode > kXSplit || plan.tiles_per_block < 1 || plan.waves < 1 ||
       plan.tiles_per_block * plan.waves > kMaxWaves[plan.xmode] ||
-      (plan.xmode != kXBlock && plan.tiles_per_block != 1) || (plan.xmode == kXWave && M > 4))
+      (plan.xmode != kXBlock && plan.xmode != kXSplit && plan.tiles_per_block != 1) ||
+      (plan.xmode == kXWave && M > 4) || plan.ranges < 1 || plan.ranges > kMaxRanges ||
+      (plan.xmode != kXSplit && plan.ranges != 1) || plan.ranges > (K + 127) / 128)
     fail("qmv: inconsistent plan");
+  const int64_t tiles = (N + 15) / 16;
+  if (plan.ranges > 1) {
+    if (!partial) fail("qmv: a plan with K ranges needs its partial-tile workspace");
+    if (plan.partial_floats < size_t(plan.ranges) * size_t(tiles) * size_t(plan.row_blocks) * 256)
+      fail("qmv: the plan's workspace is too small for its partial tiles");
+  }
   const QmvLds l = qmv_lds(plan.xmode, int(M), int(K), group_size, plan.tiles_per_block, plan.waves,
-                           plan.row_blocks);
+                           plan.row_blocks, plan.ranges);
   if (plan.xmode == kXWave && l.cmax > kXWaveMaxChunks) fail("qmv: a wave's x slice is too long to stage");
   if (l.total != plan.lds_bytes || l.total > kLdsMax) fail("qmv: plan's LDS size is wrong or too large");
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) fail("qmv: x must be 16-byte aligned");

@@ -13,6 +13,6 @@ namespace qmv_detail {
 template void qmv_combo<SDQ_XD, SDQ_SD, SDQ_OD>(int, void *, const void *, int64_t, const uint32_t *,
                                                 const void *, const void *, int, int, int, int,
                                                 const kern::QmvPlan &, const kern::Epilogue &,
-                                                hipStream_t);
+                                                hipStream_t, float *);
 } // namespace qmv_detail
 } // namespace sdq

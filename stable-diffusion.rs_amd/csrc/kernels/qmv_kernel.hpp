@@ -16,8 +16,12 @@
 //     its own LDS region, as (s, b - OFF*s) pairs, and -- at M <= 4 -- its
 //     slice of x as bf16 (XMode kXWave): no block-wide barrier stands between
 //     a wave and its stream.  For larger M with a small x the block stages x
-//     once for all its tiles (kXBlock); otherwise each wave reads its
-//     activation fragments per chunk from global memory (kXDirect).
+//     once for all its tiles (kXBlock).  When x is too large for that, K is
+//     cut into R ranges, one per block (kXSplit): a block stages its range
+//     of x once for its T tiles and stores partial tiles, which
+//     qmv_reduce_kernel adds in range order and finishes with the epilogue.
+//     Otherwise each wave reads its activation fragments per chunk from
+//     global memory (kXDirect).
 //   * MFMA v_mfma_f32_16x16x32_bf16 with the weight rows on its N side and
 //     the tokens on its M side (16 rows per MFMA row block, two blocks for
 //     M <= 32).  Lane (n, h) = (lane % 16, lane / 16) supplies weight row n
@@ -145,15 +149,48 @@ template <int BITS, int MB, bool XD> struct Chunk {
   u32x4 a[XD ? MB : 1][XD ? 4 : 1];
 };
 
+// The epilogue of one 16-row block of a tile: accumulator entry e of lane
+// (n, h) = (lane % 16, lane / 16) is token 16 mb + 4 h + e, output column
+// 16 tile + n.  Every lane of the wave takes part (the gated pair trades
+// values between lanes n and n ^ 8).
+template <int ODT>
+__device__ __forceinline__ void qmv_store_rows(typename Elem<ODT>::T *__restrict__ y, const kern::Epilogue &ep,
+                                               const floatx4 &a, int mb, int M, int N, int tile, int lane) {
+  const int ln = lane & 15, lh = lane >> 4;
+  const int n = tile * 16 + ln;
+  const float bn = epi_bias(ep, min(n, N - 1));
+  if (ep.pair) {
+    // Gated pair (kern::Epilogue::pair, N % 16 == 0): column ln < 8 of the
+    // tile is a gate, ln + 8 (lane ^ 8) its up column; output column
+    // 8 tile + ln of N / 2.
+    const int64_t ldo = ep.ldy > 0 ? ep.ldy : int64_t(N / 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float up = __shfl_xor(a[e] + bn, 8);
+      const int m = mb * 16 + 4 * lh + e;
+      if (ln < 8 && m < M) y[m * ldo + tile * 8 + ln] = Elem<ODT>::store(epi_apply(ep, a[e], bn) * up);
+    }
+    return;
+  }
+  if (n >= N) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = mb * 16 + 4 * lh + e;
+    if (m < M) *epi_dst(ep, y, N, m, n) = Elem<ODT>::store(epi_combine(ep, epi_apply_col(ep, a[e], bn, n), m, n));
+  }
+}
+
 // MB: 16-token MFMA row blocks (M <= 16 * MB).  GS: group size (64 or 128).
-// XM: where x comes from (XMode).  Launch: grid = ceil(tiles / T), T * S waves.
+// XM: where x comes from (XMode).  Launch: grid = ceil(tiles / T) (times R
+// for kXSplit, range-major), T * S waves.  partial (kXSplit, R > 1): R x
+// tiles x MB x 64 float4, the range's accumulators of each tile.
 template <int BITS, int XDT, int SDT, int ODT, int MB, int GS, int XM, int DEPTH = kDepth>
 __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
     const typename Elem<SDT>::T *__restrict__ scales,
     const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, int T, int S,
-    kern::Epilogue ep) {
+    kern::Epilogue ep, int R, float *__restrict__ partial) {
   using XT = typename Elem<XDT>::T;
   using ST = typename Elem<SDT>::T;
   constexpr bool kXD = XM == kXDirect;
@@ -173,28 +210,37 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   const int tl = wave / S;      // tile of this block
   const int rs = wave - tl * S; // K range of the tile
   const int tiles = (N + 15) / 16;
-  const int tile = int(blockIdx.x) * T + tl;
+  // kXSplit: block b takes K range rr = b / ntb of tile group tb = b % ntb.
+  constexpr bool kSplit = XM == kXSplit;
+  const int ntb = (tiles + T - 1) / T;
+  const int rr = kSplit ? int(blockIdx.x) / ntb : 0;
+  const int tb = kSplit ? int(blockIdx.x) - rr * ntb : int(blockIdx.x);
+  const int tile = tb * T + tl;
   const bool live = tile < tiles;
   const int n = tile * 16 + ln;
   const int nrow = min(n, N - 1); // rows past N are read, never stored
   const int groups = K / GS;
 
-  // This wave's chunks [c0, c1) of the 128-wide chunks and groups [g0, g1);
-  // the last chunk is half when K % 128 == 64 (group size 64).
+  // The block's chunks [b0, b1) of the 128-wide chunks (all of K but for
+  // kXSplit), this wave's [c0, c1) and groups [g0, g1); the last chunk is
+  // half when K % 128 == 64 (group size 64).
   const int nchunk = (K + 127) / 128;
-  // 32-bit products: nchunk * S < 2^31 (checked on the host).
-  const int c0 = int(uint32_t(nchunk * rs) / uint32_t(S));
-  const int c1 = int(uint32_t(nchunk * (rs + 1)) / uint32_t(S));
+  // 32-bit products: nchunk * max(S, R) < 2^31 (checked on the host).
+  const int b0 = kSplit ? int(uint32_t(nchunk * rr) / uint32_t(R)) : 0;
+  const int nb = (kSplit ? int(uint32_t(nchunk * (rr + 1)) / uint32_t(R)) : nchunk) - b0;
+  const int c0 = b0 + int(uint32_t(nb * rs) / uint32_t(S));
+  const int c1 = b0 + int(uint32_t(nb * (rs + 1)) / uint32_t(S));
   const int ncs = live ? c1 - c0 : 0;
   const bool half_tail = (K & 127) != 0;
   const int g0 = c0 * kGpc;
   const int gw = min(c1 * kGpc, groups) - g0;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const QmvLds L = qmv_lds(XM, M, K, GS, T, S, MB);
+  const QmvLds L = qmv_lds(XM, M, K, GS, T, S, MB, R);
+  constexpr bool kStaged = XM == kXBlock || XM == kXSplit; // x staged once per block
   unsigned char *wreg = smem + L.wave + wave * L.wave_bytes;
   float2 *sbw = reinterpret_cast<float2 *>(wreg);                 // [16][L.gw]
-  uint16_t *xl = reinterpret_cast<uint16_t *>(XM == kXBlock ? smem + L.x : wreg + L.wsb);
+  uint16_t *xl = reinterpret_cast<uint16_t *>(kStaged ? smem + L.x : wreg + L.wsb);
   floatx4 *red = reinterpret_cast<floatx4 *>(smem + L.red);
 
   // Buffer windows: byte offsets fit in 32 bits (checked on the host).
@@ -243,8 +289,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   constexpr bool kXPerm = BITS == 4 && !kXD;
   Chunk<BITS, MB, kXD> ring[DEPTH + 1];
   {
-    const int srow = min(int(blockIdx.x) * T * 16 + tl * 16 + ln, N - 1);
-    const uint32_t sbase = uint32_t(int64_t(srow) * groups * sizeof(ST));
+    const uint32_t sbase = uint32_t(int64_t(nrow) * groups * sizeof(ST));
     const uint32_t soff0 = uint32_t(g0) * uint32_t(sizeof(ST));
     auto put = [&](int g, float sc, float bi) {
       if (g < gw) sbw[ln * L.gw + g] = make_float2(sc, fmaf(-kOff, sc, bi));
@@ -258,14 +303,15 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
       }
     };
 
-    // (a) kXBlock: the block stages all of x, eight values per piece, for
-    //     its T tiles.  The first round of loads is held in registers and
-    //     stored after the code loads; further rounds (large x) are loaded
-    //     and stored here.
+    // (a) kXBlock, kXSplit: the block stages x (kXSplit: columns of its K
+    //     range), eight values per piece, for its T tiles.  The first round
+    //     of loads is held in registers and stored after the code loads;
+    //     further rounds (large x) are loaded and stored here.
     constexpr int kXLoads = 8;
     const int tid = int(threadIdx.x);
     const int nthreads = int(blockDim.x);
-    const int per_row = K / 8;
+    const int kx0 = b0 * 128;                         // first staged column
+    const int per_row = (min((b0 + nb) * 128, K) - kx0) / 8;
     const int x_pieces = M * per_row;
     // Row of piece e: a float estimate corrected once (exact: the estimate
     // is off by at most one for these sizes).
@@ -281,7 +327,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
       for (int j = 0; j < kXLoads; ++j) {
         const int e = min(base + j * nthreads + tid, x_pieces - 1);
         const int m = x_row(e);
-        v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + 8 * (e - m * per_row));
+        v[j] = Load8<XDT>::get(x + int64_t(m) * ldx + kx0 + 8 * (e - m * per_row));
       }
     };
     auto xb_store = [&](int base, const u32x4 (&v)[kXLoads]) {
@@ -294,8 +340,8 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
         }
       }
     };
-    u32x4 xb[XM == kXBlock ? kXLoads : 1];
-    if constexpr (XM == kXBlock) {
+    u32x4 xb[kStaged ? kXLoads : 1];
+    if constexpr (kStaged) {
       for (int base = kXLoads * nthreads; base < x_pieces; base += kXLoads * nthreads) {
         u32x4 v[kXLoads];
         xb_load(base, v);
@@ -374,7 +420,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     // (e) Stores of the staged values.  The scale form is re-read through an
     //     opaque copy, so the compiler cannot merge this branch with (c) and
     //     move these stores (and their waits) above the code loads.
-    if constexpr (XM == kXBlock) xb_store(0, xb);
+    if constexpr (kStaged) xb_store(0, xb);
     if constexpr (XM == kXWave) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -399,7 +445,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) put(lh + 4 * i, sv[i], bv[i]);
     }
-    if constexpr (XM == kXBlock) {
+    if constexpr (kStaged) {
       __syncthreads();
     } else {
       // The stage is this wave's own: a wave-scope fence orders it.
@@ -417,7 +463,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   for (int mb = 0; mb < MB; ++mb) acc[mb] = zero;
   const float2 *sbrow = sbw + ln * L.gw;
   // Column of chunk c's K range within the staged x rows.
-  const int xcol0 = XM == kXBlock ? 0 : c0 * 128;
+  const int xcol0 = kStaged ? b0 * 128 : c0 * 128;
 
   // One chunk's math: chunk i (local) of the range, codes in q.
   auto process = [&](const int i, const Chunk<BITS, MB, kXD> &q) __attribute__((always_inline)) {
@@ -531,48 +577,66 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     }
   }
 
-  // Accumulator entry e of lane (n, h) in row block mb is token
-  // 16 mb + 4 h + e, output column n of the tile.
   if (!live) return;
-  const float bn = epi_bias(ep, n);
-  if (ep.pair) {
-    // Gated pair (kern::Epilogue::pair, N % 16 == 0): column ln < 8 of the
-    // tile is a gate, ln + 8 (lane ^ 8) its up column; output column
-    // 8 tile + ln of N / 2.
-    const int64_t ldo = ep.ldy > 0 ? ep.ldy : int64_t(N / 2);
+  if constexpr (kSplit) {
+    if (R > 1) {
+      // The range's accumulators, 1 KB per wave and row block, for
+      // qmv_reduce_kernel (the next kernel on the stream).
+      floatx4 *dst = reinterpret_cast<floatx4 *>(partial) + ((int64_t(rr) * tiles + tile) * MB) * 64 + lane;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float up = __shfl_xor(acc[mb][e] + bn, 8);
-        const int m = mb * 16 + 4 * lh + e;
-        if (ln < 8 && m < M) y[m * ldo + tile * 8 + ln] = Elem<ODT>::store(epi_apply(ep, acc[mb][e], bn) * up);
-      }
-    return;
-  }
-  if (n >= N) return;
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = mb * 16 + 4 * lh + e;
-      if (m < M)
-        *epi_dst(ep, y, N, m, n) = Elem<ODT>::store(epi_combine(ep, epi_apply_col(ep, acc[mb][e], bn, n), m, n));
+      for (int mb = 0; mb < MB; ++mb) dst[mb * 64] = acc[mb];
+      return;
     }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) qmv_store_rows<ODT>(y, ep, acc[mb], mb, M, N, tile, lane);
+}
+
+// The sum of kXSplit's R partial tiles in range order (so the result does
+// not depend on which block finished first), with the epilogue.  One wave
+// per tile and row block: lane l adds float4 l of each range's slot.
+template <int ODT, int MB>
+__global__ __launch_bounds__(256) void qmv_reduce_kernel(typename Elem<ODT>::T *__restrict__ y,
+                                                         const float *__restrict__ partial, int M, int N, int R,
+                                                         kern::Epilogue ep) {
+  const int tiles = (N + 15) / 16;
+  const int lane = int(threadIdx.x) & 63;
+  const int64_t wv = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 6; // tile * MB + mb
+  if (wv >= int64_t(tiles) * MB) return;                              // whole waves
+  const int tile = int(wv / MB), mb = int(wv % MB);
+  const floatx4 *src = reinterpret_cast<const floatx4 *>(partial) + wv * 64 + lane;
+  const int64_t stride = int64_t(tiles) * MB * 64;
+  floatx4 v[kMaxRanges];
+#pragma unroll
+  for (int r = 0; r < kMaxRanges; ++r)
+    if (r < R) v[r] = src[r * stride];
+  floatx4 sum = v[0];
+#pragma unroll
+  for (int r = 1; r < kMaxRanges; ++r)
+    if (r < R)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[e] += v[r][e];
+  qmv_store_rows<ODT>(y, ep, sum, mb, M, N, tile, lane);
 }
 
 template <int BITS, int XDT, int SDT, int ODT, int MB, int GS, int XM, int DEPTH = kDepth>
 void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
                   const void *b, int M, int N, int K, const kern::QmvPlan &plan,
-                  const kern::Epilogue &ep, hipStream_t st) {
+                  const kern::Epilogue &ep, hipStream_t st, float *partial) {
   const int tiles = (N + 15) / 16;
   const int T = plan.tiles_per_block;
-  const QmvLds l = qmv_lds(XM, M, K, GS, T, plan.waves, MB);
-  const dim3 grid(unsigned((tiles + T - 1) / T));
+  const int R = XM == kXSplit ? plan.ranges : 1;
+  const QmvLds l = qmv_lds(XM, M, K, GS, T, plan.waves, MB, R);
+  const dim3 grid(unsigned((tiles + T - 1) / T * R));
   qmv_kernel<BITS, XDT, SDT, ODT, MB, GS, XM, DEPTH><<<grid, 64 * T * plan.waves, l.total, st>>>(
       static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
       w, static_cast<const typename Elem<SDT>::T *>(s), static_cast<const typename Elem<SDT>::T *>(b),
-      M, N, K, T, plan.waves, ep);
+      M, N, K, T, plan.waves, ep, R, partial);
+  if (R > 1) {
+    const int64_t threads = int64_t(tiles) * MB * 64;
+    qmv_reduce_kernel<ODT, MB><<<dim3(unsigned((threads + 255) / 256)), 256, 0, st>>>(
+        static_cast<typename Elem<ODT>::T *>(y), partial, M, N, R, ep);
+  }
 }
 
 // One activation/scale/output dtype combination of the kernel, for 4 or 8
@@ -581,45 +645,47 @@ void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w, const 
 template <int XD, int SD, int OD>
 void qmv_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
                const void *b, int M, int N, int K, int gs, const kern::QmvPlan &plan,
-               const kern::Epilogue &ep, hipStream_t st);
+               const kern::Epilogue &ep, hipStream_t st, float *partial);
 
 template <int BITS, int XD, int SD, int OD, int XM>
 void qmv_xm(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s, const void *b,
             int M, int N, int K, int gs, const kern::QmvPlan &plan, const kern::Epilogue &ep,
-            hipStream_t st) {
+            hipStream_t st, float *partial) {
   if (gs == 64) {
     if (plan.row_blocks == 1)
-      launch_qmv_t<BITS, XD, SD, OD, 1, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+      launch_qmv_t<BITS, XD, SD, OD, 1, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st, partial);
     else
-      launch_qmv_t<BITS, XD, SD, OD, 2, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+      launch_qmv_t<BITS, XD, SD, OD, 2, 64, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st, partial);
   } else {
     if (plan.row_blocks == 1)
-      launch_qmv_t<BITS, XD, SD, OD, 1, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+      launch_qmv_t<BITS, XD, SD, OD, 1, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st, partial);
     else
-      launch_qmv_t<BITS, XD, SD, OD, 2, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st);
+      launch_qmv_t<BITS, XD, SD, OD, 2, 128, XM>(y, x, ldx, w, s, b, M, N, K, plan, ep, st, partial);
   }
 }
 
 template <int BITS, int XD, int SD, int OD>
 void qmv_bits(void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s, const void *b,
               int M, int N, int K, int gs, const kern::QmvPlan &plan, const kern::Epilogue &ep,
-              hipStream_t st) {
+              hipStream_t st, float *partial) {
   if (plan.xmode == kXWave)
-    qmv_xm<BITS, XD, SD, OD, kXWave>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+    qmv_xm<BITS, XD, SD, OD, kXWave>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
   else if (plan.xmode == kXBlock)
-    qmv_xm<BITS, XD, SD, OD, kXBlock>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+    qmv_xm<BITS, XD, SD, OD, kXBlock>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
+  else if (plan.xmode == kXSplit)
+    qmv_xm<BITS, XD, SD, OD, kXSplit>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
   else
-    qmv_xm<BITS, XD, SD, OD, kXDirect>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+    qmv_xm<BITS, XD, SD, OD, kXDirect>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
 }
 
 template <int XD, int SD, int OD>
 void qmv_combo(int bits, void *y, const void *x, int64_t ldx, const uint32_t *w, const void *s,
                const void *b, int M, int N, int K, int gs, const kern::QmvPlan &plan,
-               const kern::Epilogue &ep, hipStream_t st) {
+               const kern::Epilogue &ep, hipStream_t st, float *partial) {
   if (bits == 4)
-    qmv_bits<4, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+    qmv_bits<4, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
   else
-    qmv_bits<8, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st);
+    qmv_bits<8, XD, SD, OD>(y, x, ldx, w, s, b, M, N, K, gs, plan, ep, st, partial);
 }
 
 } // namespace qmv_detail

@@ -2,8 +2,10 @@
 // for callers that cannot allocate device memory (code under HIP graph
 // capture, tight serving loops, harnesses that forbid hipMalloc).
 //
-// The only scratch memory the matmul kernels use is the large-M kernel's
-// split-K partial tiles.  Here they live in `scratch`, a file-scope device
+// The only scratch memory the matmul kernels use is the partial tiles of a
+// split K: the large-M kernel's split-K tiles and the small-M kernel's K
+// ranges (x too large for one block).  Here they live in `scratch`, a
+// file-scope device
 // array of kScratchFloats floats that every GPU the library runs on holds
 // until the process ends.  Host code never uses the array's name as an
 // address: the first call on each device takes that device's copy's address
@@ -70,10 +72,13 @@ extern "C" int sdq_quantized_matmul_noalloc(void *y, int y_dtype, const void *x,
     ep.bias_dtype = bias ? bias_dtype : 0;
     ep.act = activation;
     if (M <= 32) {
-      // The small-M kernel reduces K inside its blocks: no scratch.
-      const kern::QmvPlan plan = kern::plan_qmv(M, N, K, group_size, bits, cu_count(device));
+      // The small-M kernel's partial tiles (a large x cut into K ranges) go
+      // to the scratch when they fit; otherwise it takes a plan without.
+      kern::QmvPlan plan = kern::plan_qmv(M, N, K, group_size, bits, cu_count(device));
+      if (plan.partial_floats > kScratchFloats)
+        plan = kern::plan_qmv(M, N, K, group_size, bits, cu_count(device), false);
       kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, group_size, bits,
-                plan, ep, stream);
+                plan, ep, stream, plan.ranges > 1 ? scratch_for(device) : nullptr);
       return 0;
     }
     // The fixed scratch takes the data-parallel plan only (no stream-K flags).

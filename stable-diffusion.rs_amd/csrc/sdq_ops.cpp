@@ -83,8 +83,11 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
     fail("the quantized matmul kernels take 4 or 8 bits, got " + std::to_string(bits));
   if (M <= 32) {
     const kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, bits, cu_count(device));
+    float *partial = nullptr;
+    if (plan.ranges > 1)
+      partial = stream_workspace(device, stream, plan.partial_floats) + kWorkspaceHeaderFloats;
     kern::qmv(y, y_dtype, x, x_dtype, ldx, w, scales, biases, s_dtype, M, N, K, gs, bits,
-              plan, ep, stream);
+              plan, ep, stream, partial);
   } else {
     kern::QmmPlan plan = kern::plan_qmm(M, N, K, bits, cu_count(device));
     kern::SplitWorkspace ws;

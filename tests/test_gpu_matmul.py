@@ -220,7 +220,7 @@ def _gelu64(v):
 
 @pytest.mark.parametrize("M,N,K,bits", [
     (1, 200, 512, 4),       # small-M kernel, direct store
-    (16, 64, 8192, 8),      # small-M kernel, split K (last-arriver store)
+    (16, 64, 8192, 8),      # small-M kernel, K in ranges (the reduction kernel stores)
     (100, 300, 256, 4),     # tile kernel, whole tiles
     (300, 512, 8192, 4),    # tile kernel, split K (the reduction kernel stores)
 ])
@@ -293,7 +293,7 @@ def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
 
 @pytest.mark.parametrize("M,N,K,bits", [
     (1, 200, 512, 4),       # small-M kernel: combine in the store
-    (16, 64, 8192, 8),      # small-M kernel, split K
+    (16, 64, 8192, 8),      # small-M kernel, K in ranges: combine in the reduction kernel
     (100, 300, 256, 4),     # tile kernel: combine in its store
     (300, 512, 8192, 4),    # tile kernel with split K: combine in the reduction kernel
 ])

@@ -1,0 +1,137 @@
+"""The small-M kernel's K ranges (M <= 32 with an x too large for one block's
+LDS): each block stages one range of x for its tiles, writes partial tiles,
+and a second kernel adds them in range order with the epilogue.
+
+Against the oracle's f64 product of the dequantized weight.  The small-M
+kernel applies the affine dequantization per group in f32 on exact codes, so
+with an f32 output it agrees far inside the north star's bar (max |d| /
+max |ref| <= 2e-2, cosine >= 0.9999); the tests hold it to 1e-4, which any
+lost or doubled range, misplaced slice of x or wrong tile would break.  The
+epilogue forms (bias, GELU, gated residual, product, gated pair, split
+store) run in the reduction kernel here and are checked against the same
+forms computed from the oracle's product, and the result is bit-identical
+from call to call (ranges are added in a fixed order).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import cosine, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TIGHT = 1e-4
+
+
+def _gelu64(v):
+    c = np.float64(np.float32(0.7978845238685608))
+    return 0.5 * v * (1.0 + np.tanh((v + 0.044715 * v ** 3) * c))
+
+
+def _setup(oracle, sdq, stream, M, N, K, bits, gs, seed):
+    w = oracle.normals(seed, N * K, 0.02).reshape(N, K)
+    q = sdq.QuantizedArray.quantize(sdq.Array.from_numpy(w), gs, bits, stream)
+    wq, s, b = oracle.quantize(w, gs, bits)
+    deq = oracle.dequantize(wq, s, b, gs, bits).astype(np.float64)
+    xb = sdq.f32_to_bf16_bits(oracle.normals(seed + 1, M * K).reshape(M, K))
+    x = sdq.Array.from_numpy(xb, sdq.BFLOAT16)
+    xv = sdq.bf16_bits_to_f32(xb).reshape(M, K).astype(np.float64)
+    return q, x, xv @ deq.T
+
+
+def _close(got, want, tol=TIGHT):
+    err, cos = max_rel_err(got, want), cosine(got, want)
+    assert err <= tol and cos >= 0.9999, (err, cos)
+
+
+# (M, N, K, bits, group size): x of M x K bf16 above the 104 KB a block
+# stages whole, so the plan cuts K into ranges.
+SHAPES = [
+    (5, 256, 12288, 4, 64),     # M = 5 (one row block), two ranges
+    (13, 1040, 4096, 8, 64),    # ragged N (65 tiles), three ranges
+    (24, 512, 4160, 4, 64),     # K % 128 == 64: the last range ends in half a chunk
+    (32, 2048, 4096, 4, 128),   # group size 128, two row blocks
+    (17, 3072, 12288, 8, 64),   # Flux fc2's K at M = 17: five ranges
+    (32, 20480, 4096, 4, 64),   # T5's paired wi_0/wi_1 at M = 32
+    (16, 64, 8192, 8, 64),      # a single tile of 4 blocks' worth of K
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", SHAPES)
+def test_split_ranges_match_the_oracle(oracle, sdq, stream, M, N, K, bits, gs):
+    print(f"qmv K ranges M={M} N={N} K={K} bits={bits} gs={gs}", flush=True)
+    q, x, want = _setup(oracle, sdq, stream, M, N, K, bits, gs, 7000 + M + N)
+    y = q.matmul(x, stream)
+    assert y.dtype == sdq.FLOAT32 and y.shape == [M, N]
+    got = y.to_numpy()
+    _close(got, want)
+    # Ranges are added in a fixed order: the same bits on every call.
+    assert np.array_equal(q.matmul(x, stream).to_numpy(), got)
+
+
+def test_split_ranges_with_bf16_output(oracle, sdq, stream):
+    M, N, K = 20, 1024, 6144
+    w = oracle.normals(7100, N * K, 0.02).reshape(N, K)
+    wb = sdq.f32_to_bf16_bits(w)
+    q = sdq.QuantizedArray.quantize(sdq.Array.from_numpy(wb, sdq.BFLOAT16), 64, 4, stream)
+    wq, s, b = oracle.quantize(sdq.bf16_bits_to_f32(wb).reshape(N, K), 64, 4, 12)
+    deq = oracle.dequantize(wq, s, b, 64, 4, 12).astype(np.float64)
+    xb = sdq.f32_to_bf16_bits(oracle.normals(7101, M * K).reshape(M, K))
+    y = q.matmul(sdq.Array.from_numpy(xb, sdq.BFLOAT16), stream)
+    assert y.dtype == sdq.BFLOAT16
+    got = sdq.bf16_bits_to_f32(y.to_numpy()).reshape(M, N)
+    want = sdq.bf16_bits_to_f32(xb).reshape(M, K).astype(np.float64) @ deq.T
+    _close(got, want, 2e-2)  # one bf16 rounding of the output
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(24, 512, 4160, 4), (32, 2048, 4096, 8)])
+def test_split_ranges_epilogues(oracle, sdq, stream, M, N, K, bits):
+    print(f"qmv K ranges epilogues M={M} N={N} K={K} bits={bits}", flush=True)
+    q, x, v = _setup(oracle, sdq, stream, M, N, K, bits, 64, 7200 + M)
+    bias = oracle.normals(7201, N)
+    bias_dev = sdq.Array.from_numpy(bias)
+    _close(q.linear(x, stream, bias=bias_dev).to_numpy(), v + bias)
+    _close(q.linear(x, stream, bias=bias_dev, activation=sdq.ACT_GELU_APPROX).to_numpy(), _gelu64(v + bias))
+    r = oracle.normals(7202, M * N).reshape(M, N)
+    g = oracle.normals(7203, N)
+    r_dev, g_dev = sdq.Array.from_numpy(r), sdq.Array.from_numpy(g)
+    got = q.linear_combine(x, stream, r_dev, sdq.COMBINE_GATED_RESIDUAL, bias=bias_dev, gate=g_dev).to_numpy()
+    _close(got, r + g * (v + bias))
+    got = q.linear_combine(x, stream, r_dev, sdq.COMBINE_PRODUCT, activation=sdq.ACT_GELU_APPROX).to_numpy()
+    _close(got, _gelu64(v) * r)
+
+
+def test_split_ranges_gated_pair(oracle, sdq, stream):
+    M, N, K = 24, 1024, 8192
+    ws = [oracle.normals(7300 + i, N * K, 0.02).reshape(N, K) for i in range(2)]
+    qs = [sdq.QuantizedArray.quantize(sdq.Array.from_numpy(w), 64, 4, stream) for w in ws]
+    pair = sdq.QuantizedArray.pair(qs[0], qs[1], stream)
+    xb = sdq.f32_to_bf16_bits(oracle.normals(7302, M * K).reshape(M, K))
+    x = sdq.Array.from_numpy(xb, sdq.BFLOAT16)
+    xv = sdq.bf16_bits_to_f32(xb).reshape(M, K).astype(np.float64)
+    ys = []
+    for w in ws:
+        wq, s, b = oracle.quantize(w, 64, 4)
+        ys.append(xv @ oracle.dequantize(wq, s, b, 64, 4).astype(np.float64).T)
+    _close(pair.linear_gated(x, stream).to_numpy(), _gelu64(ys[0]) * ys[1])
+
+
+def test_split_ranges_split_store(oracle, sdq, stream):
+    M, N, K, split = 20, 1280, 6144, 768
+    q, x, v = _setup(oracle, sdq, stream, M, N, K, 4, 64, 7400)
+    ld2 = N - split + 16
+    lo = sdq.Array.from_numpy(np.zeros((M, split), np.float32))
+    hi = sdq.Array.from_numpy(np.zeros((M, ld2), np.float32))
+    stream.synchronize()
+    rc = sdq.lib().sdq_quantized_linear_split_raw(
+        lo.device_ptr, split, sdq.ACT_NONE, hi.device_ptr, ld2, sdq.ACT_GELU_APPROX, split, sdq.FLOAT32,
+        x.device_ptr, sdq.BFLOAT16, K, q.weight.device_ptr, q.scales.device_ptr, q.biases.device_ptr,
+        sdq.FLOAT32, M, N, K, 64, 4, None, 0, stream.native)
+    if rc:
+        sdq._check(rc, "split")
+    stream.synchronize()
+    _close(lo.to_numpy(), v[:, :split])
+    got_hi = hi.to_numpy()
+    _close(got_hi[:, :N - split], _gelu64(v[:, split:]))
+    assert not got_hi[:, N - split:].any()

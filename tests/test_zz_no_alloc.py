@@ -1,7 +1,7 @@
 """sdq_quantized_matmul_noalloc against sdq_quantized_matmul_epilogue_raw.
 
-Two calls in a row through the C ABI (the second on a smaller input) plus a
-small-M call: each output agrees with the allocating entry point's to the
+Two calls in a row through the C ABI (the second on a smaller input) plus
+two small-M calls (one whose K ranges use the scratch): each output agrees with the allocating entry point's to the
 north star's bar (max |d| / max |ref| <= 2e-2, cosine >= 0.9999) and with the
 oracle's f64 product on sampled rows, and the library's allocator does not
 move during the calls."""
@@ -52,6 +52,7 @@ def test_no_alloc_entry_point_matches_the_allocating_one(oracle, sdq, stream):
         (1536, 12288, 3072, 4, 4000),  # config-2 fc1: split K through the fixed scratch
         (300, 2048, 4096, 8, 4010),    # smaller: split K again, fewer partial tiles
         (8, 4096, 3072, 4, 4020),      # small M: no scratch at all
+        (24, 2048, 8192, 8, 4030),     # small M, x too large for one block: K ranges through the scratch
     ]
     built = [_case(oracle, sdq, stream, *c) for c in cases]
     active0, cache0 = sdq.active_memory(), sdq.cache_memory()
