@@ -141,7 +141,7 @@ def parse():
     ap.add_argument("--unfused", action="store_true",
                     help="report the unfused form (fc1, GELU kernel, fc2) as the headline")
     ap.add_argument("--no-config3", action="store_true")
-    ap.add_argument("--only", choices=["step", "sweep", "config3", "config5"], default=None,
+    ap.add_argument("--only", choices=["step", "sweep", "config3", "config5", "refgemm"], default=None,
                     help="run one part only (for profiling its kernels)")
     ap.add_argument("--sweep-m", default="1,4,16,32,64,128,256,512,1024,1536,4608",
                     help="comma-separated M values of the 3072->12288 sweep")
@@ -341,6 +341,36 @@ def config3(torch, raw, sdq, dev, g):
     return {"note": "T5-XXL FFN (d_model 4096, d_ff 10240; wi 4-bit, wo 8-bit, group 64): the paired gated "
                     "launch vs wi_0 with the GELU epilogue + wi_1 + an elementwise product; HIP-graph replays "
                     "over device-random weights rotated through > 512 MB", "points": rows}
+
+
+def reference_gemm(torch, dev, g):
+    """The vendor library's dense bf16 GEMM (torch.mm, hipBLASLt) on the
+    config-2/4 shapes with the weight already bf16 -- the practical MFMA
+    ceiling the quantized kernel is compared with (it also dequantizes).
+    Only with --only refgemm."""
+    rows = []
+    for (M, K, N) in [(1536, 3072, 12288), (4608, 3072, 12288), (4608, 12288, 3072), (8192, 8192, 8192)]:
+        a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        b = torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16)
+        for _ in range(5):
+            torch.mm(a, b.t())
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(20):
+                torch.mm(a, b.t())
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 20)
+        tf = 2.0 * M * N * K / best / 1e9
+        rows.append({"M": M, "K": K, "N": N, "ms": round(best, 4), "TFLOP/s": round(tf, 1),
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4)})
+        log(f"reference bf16 GEMM {M}x{K}->{N}: {best * 1e3:8.1f} us {tf:7.1f} TFLOP/s "
+            f"({tf / PEAK_BF16_TFLOPS * 100:.1f}% of peak)")
+        del a, b
+    return rows
 
 
 def cpu_baseline(args, fc1, fc2):
@@ -544,6 +574,8 @@ def main():
     if args.only in (None, "config3") and not args.no_config3:
         c3 = config3(torch, raw, sdq, dev, g)
 
+    refgemm = reference_gemm(torch, dev, g) if args.only == "refgemm" else None
+
     # ---- config 5: one Flux-schnell step's quantized linears ------------------------------------
     config5 = None
     if args.only in (None, "config5") and not args.no_config5:
@@ -632,6 +664,7 @@ def main():
         "sweep_3072x12288": sweep,
         "config3": c3,
         "config5": config5,
+        **({"reference_gemm_bf16": refgemm} if refgemm else {}),
     }
     print(json.dumps(rec), flush=True)
     return 0
