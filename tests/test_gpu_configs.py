@@ -166,18 +166,19 @@ def _host_array(sdq, vals, dt):
     return sdq.Array.from_numpy(vals.astype(np.float32)), vals.astype(np.float32)
 
 
+# (gate dtype, mode): a gate applies to the gated residual only.
+_GATE_MODES = [(g, "gated") for g in (None, "bf16", "f16", "f32")] + [(None, "product")]
+
+
 @pytest.mark.parametrize("M,N", [(100, 256), (70, 100)])   # 16-byte path, element path
 @pytest.mark.parametrize("sdt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rdt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("gdt", [None, "bf16", "f16", "f32"])
-@pytest.mark.parametrize("mode", ["gated", "product"])
+@pytest.mark.parametrize("gdt,mode", _GATE_MODES)
 def test_combine_over_operand_dtypes(oracle, sdq, stream, M, N, sdt, rdt, gdt, mode):
     # The combine stage in the large-M kernel's store (M > 32), for every output,
     # residual and gate dtype: against the f64 composition, and bit for bit
     # against the unfused sequence where that sequence rounds the same way
     # (a product, or a residual without gate: one rounding in both).
-    if mode == "product" and gdt is not None:
-        pytest.skip("a gate applies to the gated residual only")
     K = 256
     print(f"combine M={M} N={N} s={sdt} r={rdt} g={gdt} {mode}", flush=True)
     xdt = "f16" if sdt == "f16" else "bf16"
