@@ -46,6 +46,7 @@ __all__ = [
     "f32_to_bf16_bits",
     "bf16_bits_to_f32",
     "gguf_dequantize",
+    "pair_rows",
 ]
 
 LIB_PATH = Path(__file__).with_name("libsdq.so")
