@@ -71,8 +71,9 @@ template <int DT> __device__ __forceinline__ void store8(typename Elem<DT>::T *p
 enum { NORM_LAYER = 0, NORM_RMS = 1, NORM_MODULATE = 2 };
 
 // One wave per row of C values, VPL values per lane (VPL = 8 * chunks): lane
-// `lane` holds elements 8 * (64 j + lane) + 0..7 of chunk j.  vec: rows are
-// 16-byte aligned and C % 8 == 0; otherwise elements are moved one by one.
+// `lane` holds elements 8 * (64 j + lane) + 0..7 of chunk j.  vec: rows and
+// parameter arrays are 16-byte aligned and C % 8 == 0; otherwise elements are
+// moved one by one.
 //   LAYER:    y = (x - mean) * rsqrt(var + eps) [* w] [+ b]
 //   RMS:      y = x * rsqrt(mean(x^2) + eps) [* w]
 //   MODULATE: y = (x - mean) * rsqrt(var + eps) * (1 + scale[g]) + shift[g],
@@ -132,17 +133,38 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const typename Elem<XDT>
     const int c0 = 8 * (64 * j + lane);
     if (c0 >= C) break;
     float o[8];
+    if (vec && c0 + 8 <= C) {
+      // Whole chunk: the parameters come in 16-byte pieces too (vec also
+      // covers their alignment).
+      float pm[8], pa[8];
+      const typename Elem<PDT>::T *mul = MODE == NORM_MODULATE ? sc : w;
+      const typename Elem<PDT>::T *add = MODE == NORM_MODULATE ? sh : (MODE == NORM_LAYER ? bshift : nullptr);
+      if (mul) load8<PDT>(mul + c0, pm);
+      if (add) load8<PDT>(add + c0, pa);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = c0 + e < C ? c0 + e : C - 1;
-      float t = (v[j][e] - mean) * rstd;
-      if constexpr (MODE == NORM_MODULATE) {
-        t = t * (1.0f + Elem<PDT>::load(sc[c])) + Elem<PDT>::load(sh[c]);
-      } else {
-        if (w) t = t * Elem<PDT>::load(w[c]);
-        if (MODE == NORM_LAYER && bshift) t = t + Elem<PDT>::load(bshift[c]);
+      for (int e = 0; e < 8; ++e) {
+        float t = (v[j][e] - mean) * rstd;
+        if constexpr (MODE == NORM_MODULATE) {
+          t = t * (1.0f + pm[e]) + pa[e];
+        } else {
+          if (mul) t = t * pm[e];
+          if (add) t = t + pa[e];
+        }
+        o[e] = t;
       }
-      o[e] = t;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + e < C ? c0 + e : C - 1;
+        float t = (v[j][e] - mean) * rstd;
+        if constexpr (MODE == NORM_MODULATE) {
+          t = t * (1.0f + Elem<PDT>::load(sc[c])) + Elem<PDT>::load(sh[c]);
+        } else {
+          if (w) t = t * Elem<PDT>::load(w[c]);
+          if (MODE == NORM_LAYER && bshift) t = t + Elem<PDT>::load(bshift[c]);
+        }
+        o[e] = t;
+      }
     }
     if (vec && c0 + 8 <= C) {
       store8<ODT>(yr + c0, o);
@@ -256,7 +278,8 @@ void launch_norm_vpl(const void *x, void *y, int64_t rows, int C, float eps, con
   using XT = typename Elem<XDT>::T;
   using OT = typename Elem<ODT>::T;
   using PT = typename Elem<PDT>::T;
-  const bool vec = C % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool vec = C % 8 == 0 && a16(x) && a16(y) && (!w || a16(w)) && (!b || a16(b));
   const dim3 grid(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   auto *xp = static_cast<const XT *>(x);
   auto *yp = static_cast<OT *>(y);
