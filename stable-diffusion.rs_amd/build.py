@@ -111,7 +111,15 @@ def build(verbose: bool = False, jobs: int | None = None, only: list[str] | None
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
     # Longest compiles first, so the pool's tail is short.
     order = sorted(SOURCES, key=lambda s: 0 if s[0].name.startswith(("qmm", "qmv")) else 1)
-    todo = [s for s in order if only is None or s[0].name.startswith(tuple(only))]
+    # A partial build also recompiles every object older than the newest
+    # header: a changed struct seen two ways by two objects breaks at run time.
+    newest_header = max(p.stat().st_mtime for p in [*CSRC.rglob("*.hpp"), REPO / "include" / "sdq.h"])
+
+    def stale(src: Path, name: str | None) -> bool:
+        obj = _obj(src, name)
+        return not obj.exists() or obj.stat().st_mtime < newest_header
+
+    todo = [s for s in order if only is None or s[0].name.startswith(tuple(only)) or stale(s[0], s[2])]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_compile, src, extra, name, verbose) for src, extra, name in todo]
         for f in futs:

@@ -123,6 +123,8 @@ struct QmvPlan {
                            // wave, 2 staged once per block, 3 a K range
                            // staged per block (ranges > 1 blocks per tile)
   int ranges = 1;          // R: K ranges across blocks (xmode 3)
+  int row_groups = 1;      // blocks per tile group, each 16 rows of x (xmode 2,
+                           // row_blocks 1; x of all M rows too large to stage)
   int lds_bytes = 0;       // dynamic LDS of one block
   size_t partial_floats = 0; // workspace for the ranges' partial tiles
 };

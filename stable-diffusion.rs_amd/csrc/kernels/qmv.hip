@@ -37,6 +37,8 @@ constexpr int kLdsMax = 150 * 1024;       // of the CU's 160 KB
 
 namespace kern {
 
+constexpr int kern_xblock() { return qmv_detail::kXBlock; }
+
 QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus, bool allow_split) {
   using namespace qmv_detail;
   QmvPlan p;
@@ -78,6 +80,27 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
       p.tiles_per_block = int(T);
       p.waves = S;
       p.lds_bytes = bytes;
+      return p;
+    }
+  }
+  // 16 < M <= 32 with 16 rows of x small enough: two row groups, each block
+  // staging 16 rows of x for its T tiles; the two blocks of a tile group
+  // read its codes from HBM once (one XCD's L2 serves the second) and no
+  // partial tiles are written.  Measured 0-25 % faster than K ranges at
+  // K = 3072 (M = 17-32; N = 3072-21504).
+  if (M > 16 && 16 * (K + 8) * 2 <= kStageXMax) {
+    const int RG = int((M + 15) / 16);
+    const int64_t T = std::min<int64_t>((tiles * RG + ncu - 1) / ncu, 8);
+    int64_t S = (12 * ncu + tiles * RG - 1) / (tiles * RG);
+    S = std::max<int64_t>(1, std::min<int64_t>({S, kMaxWaves[kXBlock] / T, nchunk}));
+    const QmvLds l = qmv_lds(kXBlock, 16, int(K), group_size, int(T), int(S), 1);
+    if (l.total <= kLdsMax) {
+      p.xmode = kXBlock;
+      p.row_blocks = 1;
+      p.row_groups = RG;
+      p.tiles_per_block = int(T);
+      p.waves = int(S);
+      p.lds_bytes = l.total;
       return p;
     }
   }
@@ -151,7 +174,9 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
   if (N * K * bits / 8 >= lim || (M - 1) * ldx * int64_t(dtype_size(x_dtype)) + K * 4 >= lim ||
       N * (K / group_size) * int64_t(dtype_size(s_dtype)) >= lim)
     fail("qmv: x, the packed weight, scales and biases must each be under 2 GiB");
-  if (plan.row_blocks != (M <= 16 ? 1 : 2)) fail("qmv: plan's row blocks do not cover M");
+  if (plan.row_groups < 1 || plan.row_groups > 2 || (plan.row_groups > 1 && plan.xmode != kern_xblock()))
+    fail("qmv: bad row groups");
+  if (plan.row_blocks * plan.row_groups != (M <= 16 ? 1 : 2)) fail("qmv: plan's row blocks do not cover M");
   using namespace qmv_detail;
   if ((K / 128 + 1) * int64_t(std::max(plan.waves, kMaxRanges) + 1) >= lim)
     fail("qmv: K too large for the chunk arithmetic");
@@ -167,8 +192,8 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
     if (plan.partial_floats < size_t(plan.ranges) * size_t(tiles) * size_t(plan.row_blocks) * 256)
       fail("qmv: the plan's workspace is too small for its partial tiles");
   }
-  const QmvLds l = qmv_lds(plan.xmode, int(M), int(K), group_size, plan.tiles_per_block, plan.waves,
-                           plan.row_blocks, plan.ranges);
+  const QmvLds l = qmv_lds(plan.xmode, plan.row_groups > 1 ? 16 : int(M), int(K), group_size,
+                           plan.tiles_per_block, plan.waves, plan.row_blocks, plan.ranges);
   if (plan.xmode == kXWave && l.cmax > kXWaveMaxChunks) fail("qmv: a wave's x slice is too long to stage");
   if (l.total != plan.lds_bytes || l.total > kLdsMax) fail("qmv: plan's LDS size is wrong or too large");
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) fail("qmv: x must be 16-byte aligned");

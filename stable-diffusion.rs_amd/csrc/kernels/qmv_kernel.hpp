@@ -151,11 +151,12 @@ template <int BITS, int MB, bool XD> struct Chunk {
 
 // The epilogue of one 16-row block of a tile: accumulator entry e of lane
 // (n, h) = (lane % 16, lane / 16) is token 16 mb + 4 h + e, output column
-// 16 tile + n.  Every lane of the wave takes part (the gated pair trades
-// values between lanes n and n ^ 8).
+// 16 tile + n; m0 offsets the rows (row groups).  Every lane of the wave
+// takes part (the gated pair trades values between lanes n and n ^ 8).
 template <int ODT>
 __device__ __forceinline__ void qmv_store_rows(typename Elem<ODT>::T *__restrict__ y, const kern::Epilogue &ep,
-                                               const floatx4 &a, int mb, int M, int N, int tile, int lane) {
+                                               const floatx4 &a, int mb, int M, int N, int tile, int lane,
+                                               int m0 = 0) {
   const int ln = lane & 15, lh = lane >> 4;
   const int n = tile * 16 + ln;
   const float bn = epi_bias(ep, min(n, N - 1));
@@ -168,7 +169,7 @@ __device__ __forceinline__ void qmv_store_rows(typename Elem<ODT>::T *__restrict
     for (int e = 0; e < 4; ++e) {
       const float up = __shfl_xor(a[e] + bn, 8);
       const int m = mb * 16 + 4 * lh + e;
-      if (ln < 8 && m < M) y[m * ldo + tile * 8 + ln] = Elem<ODT>::store(epi_apply(ep, a[e], bn) * up);
+      if (ln < 8 && m < M) y[(m0 + m) * ldo + tile * 8 + ln] = Elem<ODT>::store(epi_apply(ep, a[e], bn) * up);
     }
     return;
   }
@@ -176,7 +177,8 @@ __device__ __forceinline__ void qmv_store_rows(typename Elem<ODT>::T *__restrict
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int m = mb * 16 + 4 * lh + e;
-    if (m < M) *epi_dst(ep, y, N, m, n) = Elem<ODT>::store(epi_combine(ep, epi_apply_col(ep, a[e], bn, n), m, n));
+    if (m < M)
+      *epi_dst(ep, y, N, m0 + m, n) = Elem<ODT>::store(epi_combine(ep, epi_apply_col(ep, a[e], bn, n), m0 + m, n));
   }
 }
 
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     int64_t ldx, const uint32_t *__restrict__ w,
     const typename Elem<SDT>::T *__restrict__ scales,
     const typename Elem<SDT>::T *__restrict__ biases, int M, int N, int K, int T, int S,
-    kern::Epilogue ep, int R, float *__restrict__ partial) {
+    kern::Epilogue ep, int R, float *__restrict__ partial, int RG) {
   using XT = typename Elem<XDT>::T;
   using ST = typename Elem<SDT>::T;
   constexpr bool kXD = XM == kXDirect;
@@ -214,7 +216,22 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   constexpr bool kSplit = XM == kXSplit;
   const int ntb = (tiles + T - 1) / T;
   const int rr = kSplit ? int(blockIdx.x) / ntb : 0;
-  const int tb = kSplit ? int(blockIdx.x) - rr * ntb : int(blockIdx.x);
+  // Row groups (kXBlock, RG > 1): block b takes rows [16 MB rg, +16 MB) of
+  // tile group tbx; the RG blocks of a tile group are 8 apart, so they run
+  // on one XCD close in time and read the group's codes from HBM once, then
+  // from that XCD's L2.  Blocks past the last tile group have no live tile.
+  int rg = 0, tbx = int(blockIdx.x);
+  if (RG > 1) {
+    rg = (tbx >> 3) % RG;
+    tbx = (tbx / (8 * RG)) * 8 + (tbx & 7);
+  }
+  const int m0 = rg * 16 * MB;           // first row of this block
+  const int Mlay = RG > 1 ? 16 * MB : M; // rows the LDS layout is sized for
+  if (RG > 1) {
+    x += int64_t(m0) * ldx;
+    M = min(M - m0, 16 * MB);
+  }
+  const int tb = kSplit ? int(blockIdx.x) - rr * ntb : tbx;
   const int tile = tb * T + tl;
   const bool live = tile < tiles;
   const int n = tile * 16 + ln;
@@ -236,7 +253,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   const int gw = min(c1 * kGpc, groups) - g0;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const QmvLds L = qmv_lds(XM, M, K, GS, T, S, MB, R);
+  const QmvLds L = qmv_lds(XM, Mlay, K, GS, T, S, MB, R);
   constexpr bool kStaged = XM == kXBlock || XM == kXSplit; // x staged once per block
   unsigned char *wreg = smem + L.wave + wave * L.wave_bytes;
   float2 *sbw = reinterpret_cast<float2 *>(wreg);                 // [16][L.gw]
@@ -589,7 +606,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     }
   }
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) qmv_store_rows<ODT>(y, ep, acc[mb], mb, M, N, tile, lane);
+  for (int mb = 0; mb < MB; ++mb) qmv_store_rows<ODT>(y, ep, acc[mb], mb, M, N, tile, lane, m0);
 }
 
 // The sum of kXSplit's R partial tiles in range order (so the result does
@@ -626,12 +643,14 @@ void launch_qmv_t(void *y, const void *x, int64_t ldx, const uint32_t *w, const 
   const int tiles = (N + 15) / 16;
   const int T = plan.tiles_per_block;
   const int R = XM == kXSplit ? plan.ranges : 1;
-  const QmvLds l = qmv_lds(XM, M, K, GS, T, plan.waves, MB, R);
-  const dim3 grid(unsigned((tiles + T - 1) / T * R));
+  const int RG = XM == kXBlock ? plan.row_groups : 1;
+  const QmvLds l = qmv_lds(XM, RG > 1 ? 16 * MB : M, K, GS, T, plan.waves, MB, R);
+  const int ntb = (tiles + T - 1) / T;
+  const dim3 grid(unsigned(RG > 1 ? (ntb + 7) / 8 * 8 * RG : ntb * R));
   qmv_kernel<BITS, XDT, SDT, ODT, MB, GS, XM, DEPTH><<<grid, 64 * T * plan.waves, l.total, st>>>(
       static_cast<typename Elem<ODT>::T *>(y), static_cast<const typename Elem<XDT>::T *>(x), ldx,
       w, static_cast<const typename Elem<SDT>::T *>(s), static_cast<const typename Elem<SDT>::T *>(b),
-      M, N, K, T, plan.waves, ep, R, partial);
+      M, N, K, T, plan.waves, ep, R, partial, RG);
   if (R > 1) {
     const int64_t threads = int64_t(tiles) * MB * 64;
     qmv_reduce_kernel<ODT, MB><<<dim3(unsigned((threads + 255) / 256)), 256, 0, st>>>(

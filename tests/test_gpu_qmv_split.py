@@ -1,6 +1,9 @@
-"""The small-M kernel's K ranges (M <= 32 with an x too large for one block's
-LDS): each block stages one range of x for its tiles, writes partial tiles,
-and a second kernel adds them in range order with the epilogue.
+"""The small-M kernel when x is too large for one block's LDS (M <= 32):
+* row groups (16 < M <= 32 and 16 rows of x fit): two blocks per tile group,
+  each staging 16 rows of x, writing its rows of y directly;
+* K ranges (otherwise): each block stages one range of x for its tiles,
+  writes partial tiles, and a second kernel adds them in range order with
+  the epilogue.
 
 Against the oracle's f64 product of the dequantized weight.  The small-M
 kernel applies the affine dequantization per group in f32 on exact codes, so
@@ -121,6 +124,63 @@ def test_split_ranges_split_store(oracle, sdq, stream):
     M, N, K, split = 20, 1280, 6144, 768
     q, x, v = _setup(oracle, sdq, stream, M, N, K, 4, 64, 7400)
     ld2 = N - split + 16
+    lo = sdq.Array.from_numpy(np.zeros((M, split), np.float32))
+    hi = sdq.Array.from_numpy(np.zeros((M, ld2), np.float32))
+    stream.synchronize()
+    rc = sdq.lib().sdq_quantized_linear_split_raw(
+        lo.device_ptr, split, sdq.ACT_NONE, hi.device_ptr, ld2, sdq.ACT_GELU_APPROX, split, sdq.FLOAT32,
+        x.device_ptr, sdq.BFLOAT16, K, q.weight.device_ptr, q.scales.device_ptr, q.biases.device_ptr,
+        sdq.FLOAT32, M, N, K, 64, 4, None, 0, stream.native)
+    if rc:
+        sdq._check(rc, "split")
+    stream.synchronize()
+    _close(lo.to_numpy(), v[:, :split])
+    got_hi = hi.to_numpy()
+    _close(got_hi[:, :N - split], _gelu64(v[:, split:]))
+    assert not got_hi[:, N - split:].any()
+
+
+# (M, N, K, bits, group size): 16 < M <= 32, x above 104 KB, 16 rows below:
+# the plan takes two row groups.
+ROW_GROUP_SHAPES = [
+    (32, 1040, 2048, 4, 64),    # ragged N (65 tiles: the last tile group partly empty)
+    (20, 512, 3072, 8, 64),     # second group of 4 rows
+    (17, 256, 3200, 4, 128),    # one row in the second group; group size 128
+    (32, 12288, 3072, 4, 64),   # the sweep's M = 32 point on Flux fc1
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", ROW_GROUP_SHAPES)
+def test_row_groups_match_the_oracle(oracle, sdq, stream, M, N, K, bits, gs):
+    print(f"qmv row groups M={M} N={N} K={K} bits={bits} gs={gs}", flush=True)
+    q, x, want = _setup(oracle, sdq, stream, M, N, K, bits, gs, 7500 + M + N)
+    got = q.matmul(x, stream).to_numpy()
+    _close(got, want)
+    assert np.array_equal(q.matmul(x, stream).to_numpy(), got)
+
+
+def test_row_groups_epilogues(oracle, sdq, stream):
+    M, N, K = 24, 1024, 3072
+    q, x, v = _setup(oracle, sdq, stream, M, N, K, 4, 64, 7600)
+    bias = oracle.normals(7601, N)
+    bias_dev = sdq.Array.from_numpy(bias)
+    _close(q.linear(x, stream, bias=bias_dev, activation=sdq.ACT_GELU_APPROX).to_numpy(), _gelu64(v + bias))
+    r = oracle.normals(7602, M * N).reshape(M, N)
+    g = oracle.normals(7603, N)
+    got = q.linear_combine(x, stream, sdq.Array.from_numpy(r), sdq.COMBINE_GATED_RESIDUAL, bias=bias_dev,
+                           gate=sdq.Array.from_numpy(g)).to_numpy()
+    _close(got, r + g * (v + bias))
+    # The gated pair and the split store through the row groups.
+    ws = [oracle.normals(7604 + i, N * K, 0.02).reshape(N, K) for i in range(2)]
+    qs = [sdq.QuantizedArray.quantize(sdq.Array.from_numpy(w), 64, 4, stream) for w in ws]
+    pair = sdq.QuantizedArray.pair(qs[0], qs[1], stream)
+    xv = sdq.bf16_bits_to_f32(sdq.f32_to_bf16_bits(oracle.normals(7601, M * K).reshape(M, K))).reshape(M, K)
+    ys = []
+    for w in ws:
+        wq, sc, bi = oracle.quantize(w, 64, 4)
+        ys.append(xv.astype(np.float64) @ oracle.dequantize(wq, sc, bi, 64, 4).astype(np.float64).T)
+    _close(pair.linear_gated(x, stream).to_numpy(), _gelu64(ys[0]) * ys[1])
+    split, ld2 = 768, N - 768 + 16
     lo = sdq.Array.from_numpy(np.zeros((M, split), np.float32))
     hi = sdq.Array.from_numpy(np.zeros((M, ld2), np.float32))
     stream.synchronize()
