@@ -143,7 +143,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
 // Tile and split-K plan of one qmm launch (a pure function of the shape and
 // the CU count).
 struct QmmPlan {
-  int bm = 256;             // rows per block tile (128 or 256); tiles are bm x 256
+  int bm = 256;             // rows per block tile (64, 128 or 256); tiles are bm x 256
   int tiles_n = 0;          // tiles along N
   int tiles = 0;            // all tiles, M-tile major
   int dp_tiles = 0;         // tiles [0, dp_tiles) are computed whole

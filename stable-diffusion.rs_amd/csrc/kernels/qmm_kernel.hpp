@@ -114,7 +114,7 @@ struct QmmWork {
 };
 
 template <int BITS, int XDT, int SDT, int ODT, int BM, int GS, bool SCH, bool SKM>
-__global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
+__global__ __launch_bounds__(kThreads, BM <= 64 ? 2 : 1) void qmm_kernel(
     typename Elem<ODT>::T *__restrict__ y, const typename Elem<XDT>::T *__restrict__ x,
     int64_t ldx, const uint32_t *__restrict__ w,
     const typename Elem<SDT>::T *__restrict__ scales,
@@ -128,7 +128,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   constexpr int kWV = BITS / 4;           // u32x4 per lane per 32-row block
   // Three stages of BM rows x 64 bf16 (128 B = 32 words per row).
   constexpr int kStage = BM * 32;
-  __shared__ __attribute__((aligned(16))) uint32_t xs[3 * kStage];
+  // The output staging reuses the LDS, 32 rows of a wave's 64 columns at a
+  // time (padded rows): at 64-row tiles that can exceed the three stages.
+  constexpr int kOutWords = 4 * 32 * (64 * int(sizeof(typename Elem<ODT>::T)) + 16) / 4;
+  constexpr int kLdsWords = 3 * kStage > kOutWords ? 3 * kStage : kOutWords;
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kLdsWords];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -292,7 +296,9 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   // pieces 0-3 each produce one pair.
   constexpr int kPieces = BITS == 4 ? 5 : 4;
   constexpr int kSlots = 2 * MB;    // MFMAs per k-step
-  constexpr int kRefillLag = 4;     // slots between an A fragment's last MFMA and its refill
+  // Slots between an A fragment's last MFMA and its refill (with two or four
+  // MFMAs per k-step every fragment is refilled for the next k-step at once).
+  constexpr int kRefillLag = kSlots >= 8 ? 4 : 0;
   uint32_t lo[2], hi[2];
   auto dq_piece = [&](const WStep &ws, int i, int j, int piece, u32x4 &dst) {
     const float sc_ = ws.s[j], bi_ = ws.b[j];
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm_kernel(
   constexpr int kChunkElems = 16 / int(sizeof(OT));
   constexpr int kCpr = 64 / kChunkElems;                 // 16-byte chunks per slab row
   constexpr int kRowBytes = 64 * int(sizeof(OT)) + 16;   // padded: no bank conflicts
-  constexpr int kWaveLds = 3 * kStage * 4 / 4;           // LDS bytes per wave
+  constexpr int kWaveLds = kLdsWords;                    // LDS bytes per wave (a quarter)
   constexpr int kPassMB = (kWaveLds / kRowBytes) / 32 >= 4 && MB % 4 == 0 ? 4
                           : (kWaveLds / kRowBytes) / 32 >= 2 && MB % 2 == 0 ? 2 : 1;
   static_assert(kPassMB * 32 * kRowBytes <= kWaveLds, "output staging exceeds the LDS");
@@ -867,7 +873,9 @@ void launch_qmm_bm(void *y, const void *x, int64_t ldx, const uint32_t *w,
                    const void *s, const void *b, int M, int N, int K, int gs,
                    const kern::QmmPlan &plan, const kern::SplitWorkspace &ws,
                    const kern::Epilogue &ep, hipStream_t st) {
-  if (plan.bm == 128)
+  if (plan.bm == 64)
+    launch_qmm_t<BITS, XDT, SDT, ODT, 64>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
+  else if (plan.bm == 128)
     launch_qmm_t<BITS, XDT, SDT, ODT, 128>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);
   else
     launch_qmm_t<BITS, XDT, SDT, ODT, 256>(y, x, ldx, w, s, b, M, N, K, gs, plan, ws, ep, st);

@@ -91,6 +91,8 @@ def test_gated_matches_the_oracle(oracle, sdq, stream, M, N, K, bits):
     (512, 10240, 4096, 4),   # T5-XXL at 512 tokens (large-M kernel, whole tiles)
     (512, 10240, 4096, 8),
     (300, 512, 8192, 4),     # split K: the pair is formed in the reduction kernel
+    (48, 10240, 4096, 4),    # 64-row tiles, split K
+    (64, 512, 256, 8),       # 64-row tiles, whole
     (200, 520, 512, 8),      # a ragged last tile (1040 paired rows)
     (4096, 1536, 12288, 4),  # stream-K (long K, tiles just short of the CUs)
 ])

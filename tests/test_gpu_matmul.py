@@ -127,6 +127,8 @@ def test_split_k_is_deterministic_and_correct(oracle, sdq, stream, M):
 @pytest.mark.parametrize("M,N,K,bits", [
     (300, 512, 8192, 4),    # 4 tiles of 256 x 256: every tile split along K
     (100, 640, 4096, 8),    # 128-row tiles, 3 tiles, split
+    (48, 640, 4096, 8),     # 64-row tiles (M <= 64), 3 tiles, split
+    (64, 12288, 3072, 4),   # Flux fc1's shape at 64 tokens: 48 tiles of 64 x 256, split
     (4352, 4096, 512, 4),   # 272 tiles: one whole round, the last 16 tiles split
 ])
 def test_large_m_split_k_is_deterministic_and_correct(oracle, sdq, stream, M, N, K, bits):
@@ -223,6 +225,8 @@ def _gelu64(v):
     (16, 64, 8192, 8),      # small-M kernel, K in ranges (the reduction kernel stores)
     (100, 300, 256, 4),     # tile kernel, whole tiles
     (300, 512, 8192, 4),    # tile kernel, split K (the reduction kernel stores)
+    (40, 300, 256, 8),      # tile kernel, 64-row tiles
+    (48, 512, 8192, 4),     # tile kernel, 64-row tiles, split K
 ])
 @pytest.mark.parametrize("act", [0, 1])
 @pytest.mark.parametrize("bias_dtype", ["f32", "bf16", None])
@@ -296,6 +300,8 @@ def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
     (16, 64, 8192, 8),      # small-M kernel, K in ranges: combine in the reduction kernel
     (100, 300, 256, 4),     # tile kernel: combine in its store
     (300, 512, 8192, 4),    # tile kernel with split K: combine in the reduction kernel
+    (40, 300, 256, 8),      # 64-row tiles: combine in the store
+    (48, 512, 8192, 4),     # 64-row tiles, split K: combine in the reduction kernel
 ])
 @pytest.mark.parametrize("mode", ["gated", "residual", "product"])
 def test_linear_combine_matches_the_composition(oracle, sdq, stream, M, N, K, bits, mode):
