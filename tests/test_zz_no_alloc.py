@@ -53,6 +53,7 @@ def test_no_alloc_entry_point_matches_the_allocating_one(oracle, sdq, stream):
         (300, 2048, 4096, 8, 4010),    # smaller: split K again, fewer partial tiles
         (8, 4096, 3072, 4, 4020),      # small M: no scratch at all
         (24, 2048, 8192, 8, 4030),     # small M, x too large for one block: K ranges through the scratch
+        (48, 6144, 4096, 4, 4040),     # 64-row tiles: split K through the scratch
     ]
     built = [_case(oracle, sdq, stream, *c) for c in cases]
     active0, cache0 = sdq.active_memory(), sdq.cache_memory()
