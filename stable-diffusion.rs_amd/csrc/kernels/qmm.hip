@@ -65,7 +65,9 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_
   // launch), plus its share of the reduction kernel, which reads every
   // partial tile once at roughly HBM speed.
   constexpr int64_t kSplitFixed = 4000;
-  constexpr int64_t kReducePerRange = 45;
+  // (A 64-row partial tile is half the bytes of the 128-row tiles the
+  // constant was measured on.)
+  const int64_t kReducePerRange = p.bm == 64 ? 23 : 45;
   p.dp_tiles = p.tiles;
   p.splits = 1;
   p.steps_per_split = int(steps);
