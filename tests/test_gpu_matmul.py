@@ -85,7 +85,7 @@ def test_bf16_scales_give_bf16_output(oracle, sdq, stream, M, bits):
     _check(sdq.bf16_bits_to_f32(y.to_numpy()), x_vals, deq)
 
 
-@pytest.mark.parametrize("M", [1, 9, 77])
+@pytest.mark.parametrize("M", [1, 9, 40, 77])
 def test_group_size_128(oracle, sdq, stream, M):
     print(f"gs128 M={M}", flush=True)
     q, deq = _qweight(oracle, sdq, stream, 700 + M, 160, 512, 4, gs=128)
@@ -94,7 +94,7 @@ def test_group_size_128(oracle, sdq, stream, M):
 
 
 @pytest.mark.parametrize("xdt", ["f16"])
-@pytest.mark.parametrize("M", [5, 70])
+@pytest.mark.parametrize("M", [5, 50, 70])
 def test_f16_activations(oracle, sdq, stream, xdt, M):
     q, deq = _qweight(oracle, sdq, stream, 750 + M, 128, 256, 8)
     x_dev, x_vals = _x(oracle, sdq, 751 + M, (M, 256), xdt)
