@@ -256,7 +256,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   const QmvLds L = qmv_lds(XM, Mlay, K, GS, T, S, MB, R);
   constexpr bool kStaged = XM == kXBlock || XM == kXSplit; // x staged once per block
   unsigned char *wreg = smem + L.wave + wave * L.wave_bytes;
-  float2 *sbw = reinterpret_cast<float2 *>(wreg);                 // [16][L.gw]
+  float2 *sbw = reinterpret_cast<float2 *>(wreg);                 // [16][L.gws]
   uint16_t *xl = reinterpret_cast<uint16_t *>(kStaged ? smem + L.x : wreg + L.wsb);
   floatx4 *red = reinterpret_cast<floatx4 *>(smem + L.red);
 
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
     const uint32_t sbase = uint32_t(int64_t(nrow) * groups * sizeof(ST));
     const uint32_t soff0 = uint32_t(g0) * uint32_t(sizeof(ST));
     auto put = [&](int g, float sc, float bi) {
-      if (g < gw) sbw[ln * L.gw + g] = make_float2(sc, fmaf(-kOff, sc, bi));
+      if (g < gw) sbw[ln * L.gws + g] = make_float2(sc, fmaf(-kOff, sc, bi));
     };
     auto pick_e = [&](const u32x4 &v, int e) -> float {
       if constexpr (sizeof(ST) == 4) {
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(64 * kMaxWaves[XM]) void qmv_kernel(
   floatx4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = zero;
-  const float2 *sbrow = sbw + ln * L.gw;
+  const float2 *sbrow = sbw + ln * L.gws;
   // Column of chunk c's K range within the staged x rows.
   const int xcol0 = kStaged ? b0 * 128 : c0 * 128;
 

@@ -29,6 +29,8 @@ struct QmvLds {
   int nb;         // most 128-wide chunks of K one block covers
   int cmax;       // most 128-wide chunks of K one wave streams
   int gw;         // groups of K one wave's scale region holds
+  int gws;        // its row stride in float2: gw made odd, so that the 16 rows
+                  // of a per-group read sit on distinct LDS banks
   int xstride;    // bf16 elements per staged x row (block or wave)
   int wsb;        // byte offset of the wave's x slice within its region
 };
@@ -39,12 +41,13 @@ __host__ __device__ inline QmvLds qmv_lds(int xmode, int M, int K, int gs, int T
   l.nb = xmode == kXSplit ? (nchunk + R - 1) / R : nchunk;
   l.cmax = (l.nb + S - 1) / S;
   l.gw = l.cmax * (128 / gs);
+  l.gws = l.gw | 1;
   // x rows are padded by 16 bytes so that the 16 rows an MFMA operand read
   // touches sit on distinct LDS banks.
   l.xstride = xmode == kXBlock ? K + 8 : xmode == kXSplit ? l.nb * 128 + 8 : l.cmax * 128 + 8;
   l.x = 0;
   l.wave = xmode == kXBlock || xmode == kXSplit ? (M * l.xstride * 2 + 15) & ~15 : 0;
-  l.wsb = (16 * l.gw * 8 + 15) & ~15;
+  l.wsb = (16 * l.gws * 8 + 15) & ~15;
   l.wave_bytes = l.wsb + (xmode == kXWave ? (M * l.xstride * 2 + 15) & ~15 : 0);
   l.red = l.wave + T * S * l.wave_bytes;
   l.total = l.red + (S > 1 ? T * S * MB * 64 * 16 : 0);
