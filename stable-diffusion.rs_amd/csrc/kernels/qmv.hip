@@ -109,8 +109,11 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
   // chunks of one tile's codes: its blocks' code chunks, their x slices
   // (read from L2, weighted 1/4) and partial tiles, slowed in proportion
   // when fewer than eight waves stream on it.  R: the fewest ranges whose
-  // slice of x fits, or one more.
-  if (allow_split && M > 4) {
+  // slice of x fits, or one more.  Up to 8 rows the waves read x directly
+  // instead (kXDirect below: no partial tiles, no second kernel), measured
+  // 2-16 % faster at M = 5-8 on Flux's fc2 and T5's wo; from 12 rows the
+  // ranges are 7-40 % faster.
+  if (allow_split && M > 8) {
     double best_cost = 0.0;
     int bestR = 0, bestT = 0, bestS = 0;
     int rmin = 0;

@@ -1,9 +1,11 @@
 """The small-M kernel when x is too large for one block's LDS (M <= 32):
 * row groups (16 < M <= 32 and 16 rows of x fit): two blocks per tile group,
   each staging 16 rows of x, writing its rows of y directly;
-* K ranges (otherwise): each block stages one range of x for its tiles,
-  writes partial tiles, and a second kernel adds them in range order with
-  the epilogue.
+* K ranges (otherwise, M > 8): each block stages one range of x for its
+  tiles, writes partial tiles, and a second kernel adds them in range order
+  with the epilogue;
+* direct x (4 < M <= 8): each wave reads its activation fragments per chunk
+  from global memory (no ranges, no second kernel).
 
 Against the oracle's f64 product of the dequantized weight.  The small-M
 kernel applies the affine dequantization per group in f32 on exact codes, so
@@ -51,7 +53,7 @@ def _close(got, want, tol=TIGHT):
 # (M, N, K, bits, group size): x of M x K bf16 above the 104 KB a block
 # stages whole, so the plan cuts K into ranges.
 SHAPES = [
-    (5, 256, 12288, 4, 64),     # M = 5 (one row block), two ranges
+    (9, 256, 12288, 4, 64),     # M = 9 (one row block), two ranges
     (13, 1040, 4096, 8, 64),    # ragged N (65 tiles), three ranges
     (24, 512, 4160, 4, 64),     # K % 128 == 64: the last range ends in half a chunk
     (32, 2048, 4096, 4, 128),   # group size 128, two row blocks
@@ -71,6 +73,27 @@ def test_split_ranges_match_the_oracle(oracle, sdq, stream, M, N, K, bits, gs):
     _close(got, want)
     # Ranges are added in a fixed order: the same bits on every call.
     assert np.array_equal(q.matmul(x, stream).to_numpy(), got)
+
+
+# (M, N, K, bits, group size): 4 < M <= 8 with x above 104 KB: each wave reads
+# its activation fragments directly (no ranges, no second kernel).
+DIRECT_SHAPES = [
+    (5, 256, 12288, 4, 64),
+    (8, 1040, 8192, 8, 64),     # ragged N
+    (7, 3072, 12288, 8, 128),   # Flux fc2's K, group size 128
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", DIRECT_SHAPES)
+def test_direct_x_matches_the_oracle(oracle, sdq, stream, M, N, K, bits, gs):
+    print(f"qmv direct x M={M} N={N} K={K} bits={bits} gs={gs}", flush=True)
+    q, x, want = _setup(oracle, sdq, stream, M, N, K, bits, gs, 7700 + M + N)
+    got = q.matmul(x, stream).to_numpy()
+    _close(got, want)
+    assert np.array_equal(q.matmul(x, stream).to_numpy(), got)
+    bias = oracle.normals(7701, N)
+    _close(q.linear(x, stream, bias=sdq.Array.from_numpy(bias), activation=sdq.ACT_GELU_APPROX).to_numpy(),
+           _gelu64(want + bias))
 
 
 def test_split_ranges_with_bf16_output(oracle, sdq, stream):
