@@ -60,7 +60,10 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
   };
   // M <= 4: each wave stages its own slice of x (no block-wide barrier).
   if (M <= 4) {
-    const int S = waves_for(1, kMaxWaves[kXWave]);
+    // More waves per tile when that brings each wave's slice of x within
+    // what it stages (long K over many tiles, e.g. T5's paired wi).
+    int S = waves_for(1, kMaxWaves[kXWave]);
+    while (S < kMaxWaves[kXWave] && S < nchunk && (nchunk + S - 1) / S > kXWaveMaxChunks) ++S;
     const QmvLds l = qmv_lds(kXWave, int(M), int(K), group_size, 1, S, p.row_blocks);
     if (l.cmax <= kXWaveMaxChunks && l.total <= kLdsMax) {
       p.xmode = kXWave;
