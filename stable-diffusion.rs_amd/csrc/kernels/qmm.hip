@@ -40,13 +40,14 @@ namespace {
 
 namespace kern {
 
-QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_partial_floats,
-                 bool allow_stream_k) {
+namespace {
+
+// The plan for tiles of `bm` rows, and its estimated cost (`*cost`, in
+// thousandths of one block's 64-wide K step at that tile height).
+QmmPlan plan_qmm_bm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_partial_floats,
+                    bool allow_stream_k, int bm, int64_t *cost) {
   QmmPlan p;
-  // 64-row tiles for M <= 64: half the MFMAs and activation staging of a
-  // 128-row tile, the same weight stream (measured 10-15 % faster at
-  // M = 33-64 on the Flux and T5 shapes).
-  p.bm = M <= 64 ? 64 : M <= 128 ? 128 : 256;
+  p.bm = bm;
   p.tiles_n = int((N + qmm_detail::kTileN - 1) / qmm_detail::kTileN);
   const int64_t tiles_m = (M + p.bm - 1) / p.bm;
   p.tiles_m = int(tiles_m);
@@ -115,6 +116,7 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_
       p.sk_workers = int(G);
       p.blocks = int(G);
       p.partial_floats = need;
+      *cost = sk_cost;
       return p;
     }
   }
@@ -134,7 +136,31 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_
     const int64_t gm = int64_t(std::lround(std::sqrt(per_xcd * ratio)));
     p.group_m = int(std::clamp<int64_t>(gm, 1, tiles_m));
   }
+  *cost = dp_cost;
   return p;
+}
+
+} // namespace
+
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int bits, int cus, size_t max_partial_floats,
+                 bool allow_stream_k) {
+  int64_t cost = 0;
+  // 64-row tiles for M <= 64: half the MFMAs and activation staging of a
+  // 128-row tile, the same weight stream (measured 10-15 % faster at
+  // M = 33-64 on the Flux and T5 shapes).
+  if (M <= 64) return plan_qmm_bm(M, N, K, bits, cus, max_partial_floats, allow_stream_k, 64, &cost);
+  if (M <= 128) return plan_qmm_bm(M, N, K, bits, cus, max_partial_floats, allow_stream_k, 128, &cost);
+  // Above 128 rows both heights are priced.  A 256-row step costs about 1.3-
+  // 1.4 times a 128-row one (measured: T5's paired wi at M = 384, one round
+  // of 64 steps either way, 100 vs 76 us), so 128-row tiles win where they
+  // fill the CUs with fewer split ranges (M = 192-640 on several Flux and T5
+  // shapes: 5-24 % faster); 256-row tiles everywhere else (M >= 768 at the
+  // Flux widths).  At 1.4 the choice matched the faster height at 20 of 24
+  // measured points, the others within 5 %.
+  int64_t c128 = 0, c256 = 0;
+  const QmmPlan p128 = plan_qmm_bm(M, N, K, bits, cus, max_partial_floats, allow_stream_k, 128, &c128);
+  const QmmPlan p256 = plan_qmm_bm(M, N, K, bits, cus, max_partial_floats, allow_stream_k, 256, &c256);
+  return c128 * 10 < c256 * 14 ? p128 : p256;
 }
 
 void qmm(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
