@@ -39,6 +39,14 @@ namespace kern {
 
 constexpr int kern_xblock() { return qmv_detail::kXBlock; }
 
+// 32 < M <= 64 in row groups against the large-M kernel (64-row tiles),
+// measured at K = 3072: 3072->3072 30-45 % faster (M = 33-64: 15.1-17.6 ->
+// 9.5-10.8 us; the tile kernel has 12 tiles to split); 3072->9216 and wider
+// 5-60 % slower.
+bool qmv_takes(int64_t M, int64_t N, int64_t K) {
+  return M <= 32 || (M <= 64 && N <= 4096 && 16 * (K + 8) * 2 <= kStageXMax);
+}
+
 QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus, bool allow_split) {
   using namespace qmv_detail;
   QmvPlan p;
@@ -77,7 +85,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
   }
   // A small x is staged once per block; blocks take several tiles when that
   // keeps the grid within one block per CU (x is then staged once per CU).
-  if (M * (K + 8) * 2 <= kStageXMax) {
+  if (M <= 32 && M * (K + 8) * 2 <= kStageXMax) {
     const int64_t T = std::min<int64_t>((tiles + ncu - 1) / ncu, 8);
     const int S = waves_for(T, kMaxWaves[kXBlock]);
     if (const int bytes = fits(kXBlock, T, S)) {
@@ -88,27 +96,31 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
       return p;
     }
   }
-  // 16 < M <= 32 with 16 rows of x small enough: two row groups, each block
-  // staging 16 rows of x for its T tiles; the two blocks of a tile group
+  // 16 < M <= 64 with 16 rows of x small enough: 2-4 row groups, each block
+  // staging 16 rows of x for its T tiles; the blocks of a tile group
   // read its codes from HBM once (one XCD's L2 serves the second) and no
   // partial tiles are written.  Measured 0-25 % faster than K ranges at
   // K = 3072 (M = 17-32; N = 3072-21504).
   if (M > 16 && 16 * (K + 8) * 2 <= kStageXMax) {
     const int RG = int((M + 15) / 16);
-    const int64_t T = std::min<int64_t>((tiles * RG + ncu - 1) / ncu, 8);
-    int64_t S = (12 * ncu + tiles * RG - 1) / (tiles * RG);
-    S = std::max<int64_t>(1, std::min<int64_t>({S, kMaxWaves[kXBlock] / T, nchunk}));
-    const QmvLds l = qmv_lds(kXBlock, 16, int(K), group_size, int(T), int(S), 1);
-    if (l.total <= kLdsMax) {
-      p.xmode = kXBlock;
-      p.row_blocks = 1;
-      p.row_groups = RG;
-      p.tiles_per_block = int(T);
-      p.waves = int(S);
-      p.lds_bytes = l.total;
-      return p;
+    // Fewer tiles per block when the block's waves would not fit the LDS.
+    for (int64_t T = std::min<int64_t>((tiles * RG + ncu - 1) / ncu, 8); T >= 1; --T) {
+      int64_t S = (12 * ncu + tiles * RG - 1) / (tiles * RG);
+      S = std::max<int64_t>(1, std::min<int64_t>({S, kMaxWaves[kXBlock] / T, nchunk}));
+      const QmvLds l = qmv_lds(kXBlock, 16, int(K), group_size, int(T), int(S), 1);
+      if (l.total <= kLdsMax) {
+        p.xmode = kXBlock;
+        p.row_blocks = 1;
+        p.row_groups = RG;
+        p.tiles_per_block = int(T);
+        p.waves = int(S);
+        p.lds_bytes = l.total;
+        return p;
+      }
     }
   }
+  // More than 32 rows only in row groups (the kernel's row blocks cover 32).
+  if (M > 32) fail("qmv: no row-group plan fits for M = " + std::to_string(M) + ", K = " + std::to_string(K));
   // A large x: K in R ranges, each staged once per block of T tiles.  The
   // shape is chosen by an estimate of the busiest CU's time, in 128-wide
   // chunks of one tile's codes: its blocks' code chunks, their x slices
@@ -170,7 +182,8 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          const uint32_t *w, const void *scales, const void *biases,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
          int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream, float *partial) {
-  if (M < 1 || M > 32) fail("qmv: M must be in [1, 32]");
+  if (M < 1 || !qmv_takes(M, N, K))
+    fail("qmv: M must be in [1, 32], or [1, 64] when N <= 4096 and 16 rows of x fit a block");
   if (N < 1 || K < 64 || K % 64 != 0) fail("qmv: bad N or K");
   if (group_size != 64 && group_size != 128) fail("qmv: group size must be 64 or 128");
   if (K % group_size != 0) fail("qmv: K % group_size != 0");
@@ -182,9 +195,11 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
   if (N * K * bits / 8 >= lim || (M - 1) * ldx * int64_t(dtype_size(x_dtype)) + K * 4 >= lim ||
       N * (K / group_size) * int64_t(dtype_size(s_dtype)) >= lim)
     fail("qmv: x, the packed weight, scales and biases must each be under 2 GiB");
-  if (plan.row_groups < 1 || plan.row_groups > 2 || (plan.row_groups > 1 && plan.xmode != kern_xblock()))
+  if (plan.row_groups < 1 || plan.row_groups > 4 || (plan.row_groups > 1 && plan.xmode != kern_xblock()))
     fail("qmv: bad row groups");
-  if (plan.row_blocks * plan.row_groups != (M <= 16 ? 1 : 2)) fail("qmv: plan's row blocks do not cover M");
+  if (plan.row_groups > 1 ? plan.row_blocks != 1 || plan.row_groups != (M + 15) / 16
+                          : M > 32 || plan.row_blocks != (M <= 16 ? 1 : 2))
+    fail("qmv: plan's row blocks do not cover M");
   using namespace qmv_detail;
   if ((K / 128 + 1) * int64_t(std::max(plan.waves, kMaxRanges) + 1) >= lim)
     fail("qmv: K too large for the chunk arithmetic");

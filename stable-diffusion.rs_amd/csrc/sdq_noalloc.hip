@@ -71,7 +71,7 @@ extern "C" int sdq_quantized_matmul_noalloc(void *y, int y_dtype, const void *x,
     ep.bias = bias;
     ep.bias_dtype = bias ? bias_dtype : 0;
     ep.act = activation;
-    if (M <= 32) {
+    if (kern::qmv_takes(M, N, K)) {
       // The small-M kernel's partial tiles (a large x cut into K ranges) go
       // to the scratch when they fit; otherwise it takes a plan without.
       kern::QmvPlan plan = kern::plan_qmv(M, N, K, group_size, bits, cu_count(device));

@@ -81,7 +81,7 @@ void matmul_dispatch(void *y, int y_dtype, const void *x, int x_dtype, int64_t l
     fail("the quantized matmul kernels take group size 64 or 128, got " + std::to_string(gs));
   if (bits != 4 && bits != 8)
     fail("the quantized matmul kernels take 4 or 8 bits, got " + std::to_string(bits));
-  if (M <= 32) {
+  if (kern::qmv_takes(M, N, K)) {
     const kern::QmvPlan plan = kern::plan_qmv(M, N, K, gs, bits, cu_count(device));
     float *partial = nullptr;
     if (plan.ranges > 1)

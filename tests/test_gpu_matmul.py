@@ -128,7 +128,7 @@ def test_split_k_is_deterministic_and_correct(oracle, sdq, stream, M):
     (300, 512, 8192, 4),    # 4 tiles of 256 x 256: every tile split along K
     (100, 640, 4096, 8),    # 128-row tiles, 3 tiles, split
     (48, 640, 4096, 8),     # 64-row tiles (M <= 64), 3 tiles, split
-    (64, 12288, 3072, 4),   # Flux fc1's shape at 64 tokens: 48 tiles of 64 x 256, split
+    (64, 12288, 4096, 4),   # 64 tokens at K = 4096: 48 tiles of 64 x 256, split
     (4352, 4096, 512, 4),   # 272 tiles: one whole round, the last 16 tiles split
 ])
 def test_large_m_split_k_is_deterministic_and_correct(oracle, sdq, stream, M, N, K, bits):
