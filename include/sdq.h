@@ -241,7 +241,7 @@ typedef enum sdq_combine_ {
  * linear at those call sites.  residual: the output's shape, any float
  * dtype; gate: N values or a NULL-ctx handle.  The whole epilogue runs in
  * the matmul's store (or in the reduction of split-K tiles): in the small-M
- * kernel (M <= 32, or up to 64 rows when N <= 4096 and K <= 3320) on the
+ * kernel (M <= 32, or up to 128 rows when N <= 4096 and K <= 3320) on the
  * f32 value; in the large-M kernel the combine stage takes v rounded to the
  * output dtype (as the unfused sequence does). */
 int sdq_quantized_linear_combine(sdq_array *res, sdq_array x, sdq_array w,

@@ -129,11 +129,11 @@ struct QmvPlan {
   size_t partial_floats = 0; // workspace for the ranges' partial tiles
 };
 
-// y [M, N] = x [M, K] @ dequantize(w).T for M <= 32 (up to 64 in row groups,
+// y [M, N] = x [M, K] @ dequantize(w).T for M <= 32 (up to 128 in row groups,
 // see qmv_takes).  qmv.hip.  With
 // allow_split false the plan needs no workspace (ranges == 1).
 // Whether the small-M kernel takes an M x K activation against N weight
-// rows: M <= 32, or up to 64 rows in row groups of 16 when 16 rows of x fit
+// rows: M <= 32, or up to 128 rows in row groups of 16 when 16 rows of x fit
 // one block's stage and N is small (the large-M kernel has few tiles there).
 bool qmv_takes(int64_t M, int64_t N, int64_t K);
 QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus,

@@ -39,12 +39,13 @@ namespace kern {
 
 constexpr int kern_xblock() { return qmv_detail::kXBlock; }
 
-// 32 < M <= 64 in row groups against the large-M kernel (64-row tiles),
-// measured at K = 3072: 3072->3072 30-45 % faster (M = 33-64: 15.1-17.6 ->
-// 9.5-10.8 us; the tile kernel has 12 tiles to split); 3072->9216 and wider
-// 5-60 % slower.
+// 32 < M <= 128 in 3-8 row groups against the large-M kernel, measured at
+// K = 2048-3072: 3072->3072 30-45 % faster (M = 33-64: 15.1-17.6 -> 9.5-10.8
+// us, M = 65-128: 19.4-23.5 -> 11.0-15.9 us; the tile kernel has 12 tiles to
+// split), 2048->1024 about 2x, 3072->4096 even; 3072->9216 and wider 5-60 %
+// slower.
 bool qmv_takes(int64_t M, int64_t N, int64_t K) {
-  return M <= 32 || (M <= 64 && N <= 4096 && 16 * (K + 8) * 2 <= kStageXMax);
+  return M <= 32 || (M <= 128 && N <= 4096 && 16 * (K + 8) * 2 <= kStageXMax);
 }
 
 QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int cus, bool allow_split) {
@@ -96,7 +97,7 @@ QmvPlan plan_qmv(int64_t M, int64_t N, int64_t K, int group_size, int bits, int 
       return p;
     }
   }
-  // 16 < M <= 64 with 16 rows of x small enough: 2-4 row groups, each block
+  // 16 < M <= 128 with 16 rows of x small enough: 2-8 row groups, each block
   // staging 16 rows of x for its T tiles; the blocks of a tile group
   // read its codes from HBM once (one XCD's L2 serves the second) and no
   // partial tiles are written.  Measured 0-25 % faster than K ranges at
@@ -183,7 +184,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
          int s_dtype, int64_t M, int64_t N, int64_t K, int group_size,
          int bits, const QmvPlan &plan, const Epilogue &ep, hipStream_t stream, float *partial) {
   if (M < 1 || !qmv_takes(M, N, K))
-    fail("qmv: M must be in [1, 32], or [1, 64] when N <= 4096 and 16 rows of x fit a block");
+    fail("qmv: M must be in [1, 32], or [1, 128] when N <= 4096 and 16 rows of x fit a block");
   if (N < 1 || K < 64 || K % 64 != 0) fail("qmv: bad N or K");
   if (group_size != 64 && group_size != 128) fail("qmv: group size must be 64 or 128");
   if (K % group_size != 0) fail("qmv: K % group_size != 0");
@@ -195,7 +196,7 @@ void qmv(void *y, int y_dtype, const void *x, int x_dtype, int64_t ldx,
   if (N * K * bits / 8 >= lim || (M - 1) * ldx * int64_t(dtype_size(x_dtype)) + K * 4 >= lim ||
       N * (K / group_size) * int64_t(dtype_size(s_dtype)) >= lim)
     fail("qmv: x, the packed weight, scales and biases must each be under 2 GiB");
-  if (plan.row_groups < 1 || plan.row_groups > 4 || (plan.row_groups > 1 && plan.xmode != kern_xblock()))
+  if (plan.row_groups < 1 || plan.row_groups > 8 || (plan.row_groups > 1 && plan.xmode != kern_xblock()))
     fail("qmv: bad row groups");
   if (plan.row_groups > 1 ? plan.row_blocks != 1 || plan.row_groups != (M + 15) / 16
                           : M > 32 || plan.row_blocks != (M <= 16 ? 1 : 2))

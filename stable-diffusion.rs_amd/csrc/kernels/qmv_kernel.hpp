@@ -1,5 +1,5 @@
 // qmv_kernel.hpp -- y = x @ dequantize(w).T for few rows of x (M <= 32, up to
-// 64 in row groups of 16): the
+// 128 in row groups of 16): the
 // bandwidth-bound decode/modulation shape of mlx_quantized_matmul
 // (crates/sd-tensor/src/mlx.rs:386-397, 1947-1975; callers e.g. the Flux
 // modulation linears at M = 1, sd-models/src/mlx/flux.rs:279-299, 437, and the

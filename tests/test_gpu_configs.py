@@ -170,12 +170,12 @@ def _host_array(sdq, vals, dt):
 _GATE_MODES = [(g, "gated") for g in (None, "bf16", "f16", "f32")] + [(None, "product")]
 
 
-@pytest.mark.parametrize("M,N", [(100, 256), (70, 100)])   # 16-byte path, element path
+@pytest.mark.parametrize("M,N", [(160, 256), (150, 100)])   # 16-byte path, element path
 @pytest.mark.parametrize("sdt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rdt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("gdt,mode", _GATE_MODES)
 def test_combine_over_operand_dtypes(oracle, sdq, stream, M, N, sdt, rdt, gdt, mode):
-    # The combine stage in the large-M kernel's store (M > 32), for every output,
+    # The combine stage in the large-M kernel's store (M > 128 here), for every output,
     # residual and gate dtype: against the f64 composition, and bit for bit
     # against the unfused sequence where that sequence rounds the same way
     # (a product, or a residual without gate: one rounding in both).

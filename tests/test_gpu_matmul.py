@@ -223,7 +223,8 @@ def _gelu64(v):
 @pytest.mark.parametrize("M,N,K,bits", [
     (1, 200, 512, 4),       # small-M kernel, direct store
     (16, 64, 8192, 8),      # small-M kernel, K in ranges (the reduction kernel stores)
-    (100, 300, 256, 4),     # tile kernel, whole tiles
+    (100, 300, 256, 4),     # narrow layer: the small-M kernel's row groups
+    (100, 300, 4096, 4),    # tile kernel, 128-row tiles
     (300, 512, 8192, 4),    # tile kernel, split K (the reduction kernel stores)
     (40, 300, 256, 8),      # tile kernel, 64-row tiles
     (48, 512, 8192, 4),     # tile kernel, 64-row tiles, split K
@@ -298,7 +299,8 @@ def test_linear_epilogue_rejects_bad_arguments(oracle, sdq, stream):
 @pytest.mark.parametrize("M,N,K,bits", [
     (1, 200, 512, 4),       # small-M kernel: combine in the store
     (16, 64, 8192, 8),      # small-M kernel, K in ranges: combine in the reduction kernel
-    (100, 300, 256, 4),     # tile kernel: combine in its store
+    (100, 300, 256, 4),     # narrow layer: row groups, combine in their store
+    (100, 300, 4096, 4),    # tile kernel: combine in its store
     (300, 512, 8192, 4),    # tile kernel with split K: combine in the reduction kernel
     (40, 300, 256, 8),      # 64-row tiles: combine in the store
     (48, 512, 8192, 4),     # 64-row tiles, split K: combine in the reduction kernel

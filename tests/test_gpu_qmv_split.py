@@ -1,7 +1,8 @@
 """The small-M kernel when x is too large for one block's LDS (M <= 32, or
-M <= 64 in row groups):
-* row groups (16 < M <= 64 and 16 rows of x fit): two to four blocks per
-  tile group, each staging 16 rows of x, writing its rows of y directly;
+M <= 128 in row groups on narrow layers):
+* row groups (16 < M <= 32, or up to 128 at N <= 4096, and 16 rows of x
+  fit): two to eight blocks per tile group, each staging 16 rows of x,
+  writing its rows of y directly;
 * K ranges (otherwise, M > 8): each block stages one range of x for its
   tiles, writes partial tiles, and a second kernel adds them in range order
   with the epilogue;
@@ -174,6 +175,8 @@ ROW_GROUP_SHAPES = [
     (48, 1040, 2048, 4, 64),    # three row groups, ragged N
     (40, 512, 3200, 4, 128),    # three groups, 8 rows in the last; group size 128
     (64, 3072, 3072, 8, 64),    # four row groups (the sweep's M = 64 at N = 3072)
+    (80, 1040, 2048, 4, 64),    # five row groups, ragged N
+    (128, 3072, 3072, 4, 64),   # eight row groups
 ]
 
 
@@ -186,7 +189,7 @@ def test_row_groups_match_the_oracle(oracle, sdq, stream, M, N, K, bits, gs):
     assert np.array_equal(q.matmul(x, stream).to_numpy(), got)
 
 
-@pytest.mark.parametrize("M", [24, 56])
+@pytest.mark.parametrize("M", [24, 56, 120])
 def test_row_groups_epilogues(oracle, sdq, stream, M):
     N, K = 1024, 3072
     q, x, v = _setup(oracle, sdq, stream, M, N, K, 4, 64, 7600)
